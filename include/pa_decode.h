@@ -1,0 +1,155 @@
+/*
+ * pa_decode.h - C ABI of the MI355X (gfx950) paged-attention decode library
+ * (libpa_decode.so).
+ *
+ * One operator: single-query decode attention over a paged KV cache with
+ * grouped-query attention (GQA),
+ *
+ *   out[b, h, :] = softmax(scale * q[b, h, :] . K_b^T) . V_b
+ *
+ * where K_b / V_b are the first seq_lens[b] tokens of the pages listed in
+ * block_table[b, :], and kv head = h / (num_q_heads / num_kv_heads).
+ * A row with seq_lens[b] == 0 produces zeros.
+ *
+ * Tensor layouts (element strides, all int64):
+ *   q           fp16 [batch, num_q_heads, head_dim]
+ *   k_cache     fp16 [num_pages, page_size, num_kv_heads, head_dim]
+ *   v_cache     fp16 [num_pages, page_size, num_kv_heads, head_dim]
+ *   block_table int32 [batch, max_pages]
+ *   seq_lens    int32 [batch]
+ *   out         fp16 [batch, num_q_heads, head_dim]
+ * head_dim must be contiguous (stride 1) for q, k_cache, v_cache and out.
+ *
+ * The library replaces the reference's native launcher
+ *   torch::Tensor paged_attn_decode_cuda_v4_launch(q, k_cache, v_cache,
+ *       block_table, seq_lens, scale, gqa_ratio, head_dim, page_size,
+ *       num_splits)
+ * declared at cuda/kernels.h:60-70 and defined at
+ * cuda/kernel_v4_split_k.cu:205-268, bound to Python as `forward_v4`
+ * (cuda/binding.cpp:13-14).  Unlike that launcher, nothing here allocates:
+ * the caller passes the output and a workspace sized by
+ * pad_decode_workspace_bytes(), and the launch is asynchronous on the
+ * caller's stream with no host synchronisation.
+ *
+ * Every entry point returns a pad_status.  Host-only functions
+ * (pad_decode_plan, pad_decode_workspace_bytes, pad_status_string,
+ * pad_decode_abi_version) touch no device and can be called without a GPU.
+ */
+#ifndef PA_DECODE_H_
+#define PA_DECODE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PAD_ABI_VERSION 1
+
+/* Largest supported GQA group (query heads per KV head); the reference's
+ * bound is the same (cuda/kernel_v4_split_k.cu:44). */
+#define PAD_MAX_GQA 16
+/* Largest split count one call may use (bounded by phase-2 LDS). */
+#define PAD_MAX_SPLITS 1024
+
+typedef enum pad_status {
+  PAD_OK = 0,
+  PAD_ERR_NULL_POINTER = 1,      /* a required pointer is NULL            */
+  PAD_ERR_INVALID_SHAPE = 2,     /* non-positive or inconsistent sizes    */
+  PAD_ERR_UNSUPPORTED_HEAD_DIM = 3, /* head_dim not in {32,64,96,128,256}  */
+  PAD_ERR_UNSUPPORTED_GQA = 4,   /* num_q_heads % num_kv_heads != 0 or
+                                    group larger than PAD_MAX_GQA          */
+  PAD_ERR_STRIDE = 5,            /* head_dim stride != 1                   */
+  PAD_ERR_ALIGNMENT = 6,         /* K/V/q/out rows not 16-byte aligned     */
+  PAD_ERR_WORKSPACE = 7,         /* workspace NULL or too small            */
+  PAD_ERR_NUM_SPLITS = 8,        /* num_splits < 0 or > PAD_MAX_SPLITS     */
+  PAD_ERR_LAUNCH = 9,            /* the HIP runtime rejected a launch      */
+  PAD_ERR_DEVICE = 10            /* no usable device / device query failed */
+} pad_status;
+
+/* Shapes and element strides of one call (a plain tensor descriptor). */
+typedef struct pad_decode_dims {
+  int32_t batch;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t page_size;
+  int32_t max_pages;        /* block_table.shape[1]                        */
+  int64_t num_pages;        /* k_cache.shape[0]; not read on the device    */
+  int64_t q_stride[3];      /* [batch, head, dim]                          */
+  int64_t k_stride[4];      /* [page, slot, kv_head, dim]                  */
+  int64_t v_stride[4];
+  int64_t bt_stride[2];     /* [batch, page column]                        */
+  int64_t sl_stride;        /* seq_lens[b] is at seq_lens + b * sl_stride  */
+  int64_t out_stride[3];
+} pad_decode_dims;
+
+/* Work decomposition chosen for a call: the kernels walk
+ * pages_per_split pages of one sequence per workgroup. */
+typedef struct pad_decode_plan_t {
+  int32_t num_splits;       /* splits per (sequence, kv head)              */
+  int32_t pages_per_split;
+  int32_t waves_per_group;  /* 64-lane waves per phase-1 workgroup         */
+  int32_t single_pass;      /* 1: phase 1 writes `out`, no phase 2         */
+  int32_t engine;           /* 0 = MFMA tiles, 1 = VALU/DPP dot products   */
+  int32_t reserved;
+  size_t workspace_bytes;   /* fp32 partial (O, m, l) bytes; 0 if single   */
+} pad_decode_plan_t;
+
+/* Choose the split count and workgroup shape.  num_splits > 0 forces that
+ * many splits (the reference's `num_splits` argument,
+ * src/kernel_cuda_v4.py:19-27); 0 selects the built-in heuristic, which
+ * depends only on shapes and the CU count (num_cus <= 0 means 256).  Pure
+ * host function: it reads neither seq_lens nor block_table.  Replaces the
+ * reference's fixed default _DEFAULT_NUM_SPLITS = 64
+ * (src/kernel_cuda_v4.py:16). */
+int pad_decode_plan(const pad_decode_dims* dims, int num_splits, int num_cus,
+                    pad_decode_plan_t* plan);
+
+/* Bytes of workspace pad_decode_launch() needs for these arguments
+ * (0 when the plan is single-pass).  Pure host function.  The reference
+ * allocated the same partials per call inside its launcher
+ * (cuda/kernel_v4_split_k.cu:228-232). */
+int pad_decode_workspace_bytes(const pad_decode_dims* dims, int num_splits,
+                               int num_cus, size_t* bytes);
+
+/* Launch the decode on `stream` (a hipStream_t; NULL = the null stream).
+ * Asynchronous: returns once the kernels are queued.  `scale` is the
+ * softmax scale (the reference defaults it to 1/sqrt(head_dim),
+ * src/kernel_cuda_v4.py:60).  `num_splits` as in pad_decode_plan().
+ * Replaces paged_attn_decode_cuda_v4_launch
+ * (cuda/kernel_v4_split_k.cu:205-268). */
+int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache,
+                      const int32_t* block_table, const int32_t* seq_lens,
+                      void* out, void* workspace, size_t workspace_bytes,
+                      const pad_decode_dims* dims, float scale,
+                      int num_splits, void* stream);
+
+/* Same as pad_decode_launch(), with the engine forced (0 = MFMA tiles,
+ * 1 = VALU/DPP dot products) and, when `events` is not NULL, three
+ * hipEvent_t handles recorded on `stream` before phase 1, after phase 1
+ * and after phase 2 (the third equals the second when single-pass).  For
+ * measurement; the outputs are the same as pad_decode_launch()'s.  No
+ * counterpart in the reference. */
+int pad_decode_launch_ex(const void* q, const void* k_cache,
+                         const void* v_cache, const int32_t* block_table,
+                         const int32_t* seq_lens, void* out, void* workspace,
+                         size_t workspace_bytes, const pad_decode_dims* dims,
+                         float scale, int num_splits, int engine,
+                         void* const* events, void* stream);
+
+/* Compute units of the current device (cached per device). */
+int pad_device_num_cus(int* num_cus);
+
+/* Static text for a status code. */
+const char* pad_status_string(int status);
+
+/* PAD_ABI_VERSION of the built library. */
+int pad_decode_abi_version(void);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* PA_DECODE_H_ */

@@ -1,0 +1,26 @@
+"""MI355X-native paged-attention decode.
+
+Drop-in replacement for the decode operator of Kare0638/paged-attention-decode
+(``paged_attention_decode_cuda_v4``, src/kernel_cuda_v4.py:19-65), running
+hand-written gfx950 HIP kernels through the C ABI in include/pa_decode.h.
+"""
+
+from .ops import (  # noqa: F401
+    ENGINE_MFMA,
+    ENGINE_VALU,
+    SUPPORTED_HEAD_DIMS,
+    paged_attention_decode,
+    paged_attention_decode_cuda_v4,
+    paged_attention_decode_ex,
+    plan,
+)
+
+__all__ = [
+    "paged_attention_decode",
+    "paged_attention_decode_cuda_v4",
+    "paged_attention_decode_ex",
+    "plan",
+    "ENGINE_MFMA",
+    "ENGINE_VALU",
+    "SUPPORTED_HEAD_DIMS",
+]

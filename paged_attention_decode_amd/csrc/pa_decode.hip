@@ -1,0 +1,889 @@
+// pa_decode.hip - gfx950 (MI355X) paged-attention decode: kernels + C ABI.
+//
+// Operator contract: the reference oracle paged_attention_decode_reference
+// (src/reference.py:8-54) evaluated on fp16 inputs, output in fp16.
+// Work decomposition: split-K over the sequence ("FlashDecoding"), the same
+// merge algebra as analysis/split_k_derivation.md:16-86, restated here:
+//
+//   phase 1, per (sequence b, kv head, split s) over its tokens:
+//     m_s = max score,  l_s = sum exp(score - m_s),
+//     O_s = sum exp(score - m_s) * V                  (not divided by l_s)
+//   phase 2, per (b, q head):
+//     m = max_s m_s,  w_s = exp(m_s - m) (0 for an empty split),
+//     out = (sum_s w_s O_s) / (sum_s w_s l_s)
+//
+// Scores are kept in base-2 units (score * scale * log2 e) so every
+// exponential is a single v_exp_f32 (exp(x) = 2^(x log2 e)).
+//
+// Design (MI355X-first, not a translation of the reference's kernels):
+//  * Splits are page-aligned: split s of a sequence covers logical pages
+//    [s*pages_per_split, (s+1)*pages_per_split), so each page and each
+//    block_table entry is read by exactly one workgroup.  The reference
+//    split by tokens (cuda/kernel_v4_split_k.cu:73-75).
+//  * A phase-1 workgroup is 1-4 wave64s; each wave walks 16-token blocks of
+//    its split and keeps its own online-softmax state; the waves' states are
+//    merged through LDS at the end (one fp32 partial per workgroup).
+//  * Engine 0 (MFMA): scores are computed transposed, S^T = K . Q^T, with
+//    v_mfma_f32_16x16x16_f16 (16 tokens x 16 padded GQA rows, K = head_dim),
+//    and the output as O^T = V^T . P^T.  With S^T every lane already holds
+//    P^T in the B-operand layout of the PV product, so P never moves between
+//    lanes.  The head_dim index inside each MFMA tile is permuted so that
+//    every lane's K and V operands are 16-byte loads straight from HBM:
+//    K rows are read 64 contiguous bytes per token per instruction and V
+//    rows 256 contiguous bytes per token per instruction.  One K/V tile is
+//    shared by the whole GQA group through the MFMA B operand.
+//  * Engine 1 (VALU): 16 lanes per token, fp16x2 dot products
+//    (v_dot2_f32_f16) reduced across the 16 lanes with 4 DPP steps, fp32
+//    online softmax and FMA accumulation of P.V.  Kept for the measured
+//    comparison against engine 0.
+//  * Phase 2 runs one 256-thread workgroup per (b, q head), parallel over
+//    splits and head_dim, with the -inf guard on every split weight.  When a
+//    single split covers every sequence, phase 1 normalises and writes the
+//    fp16 output itself and phase 2 is not launched.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "pa_decode.h"
+
+namespace pad {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kBlockTokens = 16;  // tokens per wave iteration (one MFMA tile)
+constexpr int kMaxWaves = 4;
+constexpr int kPhase2Threads = 256;
+constexpr int kMergeLdsBudget = 48 * 1024;  // bytes of LDS for the wave merge
+
+struct Phase1Args {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* v;
+  const int32_t* bt;
+  const int32_t* sl;
+  _Float16* out;
+  float* o_part;   // [B, Hkv, S, gqa, D]
+  float2* ml_part; // [B, Hkv, S, gqa]  (m in base-2 units, l)
+  int64_t sqb, sqh;
+  int64_t skp, sks, skh;
+  int64_t svp, svs, svh;
+  int64_t sbb, sbp;
+  int64_t ssl;
+  int64_t sob, soh;
+  int64_t num_pages;
+  int gqa, ps, pps, num_splits, hkv, max_pages;
+  int single;  // 1: this launch covers whole sequences and writes `out`
+  float scale_log2;
+};
+
+struct Phase2Args {
+  const float* o_part;
+  const float2* ml_part;
+  const int32_t* sl;
+  _Float16* out;
+  int64_t ssl, sob, soh;
+  int gqa, ps, pps, num_splits, hkv, max_pages;
+};
+
+__device__ __forceinline__ float exp2_fast(float x) {
+  return __builtin_amdgcn_exp2f(x);  // v_exp_f32; exp2(-inf) = 0
+}
+
+__device__ __forceinline__ float shfl_xor_f(float x, int m) {
+  return __shfl_xor(x, m, 64);
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), result in all.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));  // row_half_mirror
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));  // row_mirror
+  return x;
+}
+
+// NDW dwords (2*NDW halves) loaded from a 4*NDW-byte aligned address.
+template <int NDW>
+struct HVec {
+  uint32_t w[NDW];
+  __device__ __forceinline__ _Float16 h(int i) const {
+    const uint32_t x = w[i >> 1];
+    const uint16_t bits = (i & 1) ? (uint16_t)(x >> 16) : (uint16_t)(x & 0xffffu);
+    return __builtin_bit_cast(_Float16, bits);
+  }
+  __device__ __forceinline__ h2_t h2(int i) const { return __builtin_bit_cast(h2_t, w[i]); }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < NDW; ++i) w[i] = 0u;
+  }
+};
+
+template <int NDW>
+__device__ __forceinline__ HVec<NDW> load_hvec(const _Float16* p) {
+  HVec<NDW> r;
+  if constexpr (NDW % 4 == 0) {
+    const uint4* src = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < NDW / 4; ++i) {
+      const uint4 x = src[i];
+      r.w[4 * i + 0] = x.x; r.w[4 * i + 1] = x.y; r.w[4 * i + 2] = x.z; r.w[4 * i + 3] = x.w;
+    }
+  } else if constexpr (NDW % 2 == 0) {
+    const uint2* src = reinterpret_cast<const uint2*>(p);
+#pragma unroll
+    for (int i = 0; i < NDW / 2; ++i) {
+      const uint2 x = src[i];
+      r.w[2 * i + 0] = x.x; r.w[2 * i + 1] = x.y;
+    }
+  } else {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+    for (int i = 0; i < NDW; ++i) r.w[i] = src[i];
+  }
+  return r;
+}
+
+__device__ __forceinline__ int clamp_page(int phys, int64_t num_pages) {
+  // Keeps every access inside the cache for an invalid block_table entry
+  // (the reference documents valid ids as a precondition and does not
+  // check them on the device; here a bad id reads page 0 instead of
+  // faulting).
+  return (phys < 0 || (int64_t)phys >= num_pages) ? 0 : phys;
+}
+
+// ---------------------------------------------------------------------------
+// Per-wave state handed to the workgroup merge, written to LDS in one format
+// for both engines:  sm_ml[w*16 + row] = (m, l),  sm_o[(w*gqa + row)*D + d].
+// ---------------------------------------------------------------------------
+
+// Engine 0: MFMA 16x16x16 f16 tiles.
+template <int D, bool UNIFORM>
+__device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int b, int kvh, int t_begin,
+                                               int t_end, int nblk, int wave, int nw, int lane,
+                                               float2* sm_ml, float* sm_o) {
+  constexpr int DK = D / 32;  // 16-byte K chunks per lane per token
+  constexpr int DT = D / 16;  // PV output tiles; V halves per lane per token
+  constexpr int NDW = DT / 2;
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+  const bool row_ok = r16 < a.gqa;
+
+  // Q^T operand (B of S^T = K.Q^T): row r16, head_dim slots kp*32 + g*8 + [0,8).
+  h8_t qv[DK];
+  {
+    const _Float16* qrow = a.q + (int64_t)b * a.sqb + (int64_t)(kvh * a.gqa + (row_ok ? r16 : 0)) * a.sqh;
+#pragma unroll
+    for (int kp = 0; kp < DK; ++kp) {
+      h8_t x = *reinterpret_cast<const h8_t*>(qrow + kp * 32 + g * 8);
+      qv[kp] = row_ok ? x : (h8_t)0;
+    }
+  }
+
+  float m_run = kNegInf;
+  float l_run = 0.f;
+  f4_t o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = (f4_t)0.f;
+
+  const int64_t koff_h = (int64_t)kvh * a.skh;
+  const int64_t voff_h = (int64_t)kvh * a.svh;
+  const int32_t* bt_row = a.bt + (int64_t)b * a.sbb;
+
+  for (int j = wave; j < nblk; j += nw) {
+    const int t0 = t_begin + j * kBlockTokens;
+    const bool full = t0 + kBlockTokens <= t_end;
+    const _Float16* krow;
+    const _Float16* vrow[4];
+    if constexpr (UNIFORM) {
+      // page_size % 16 == 0 and splits start on page boundaries: the whole
+      // block lives in one page, so the page id is wave-uniform.
+      const int page = t0 / a.ps;
+      const int phys = clamp_page(__builtin_amdgcn_readfirstlane(bt_row[(int64_t)page * a.sbp]), a.num_pages);
+      const int slot0 = t0 - page * a.ps;
+      const _Float16* kbase = a.k + (int64_t)phys * a.skp + koff_h + (int64_t)slot0 * a.sks;
+      const _Float16* vbase = a.v + (int64_t)phys * a.svp + voff_h + (int64_t)slot0 * a.svs;
+      krow = kbase + (int64_t)r16 * a.sks;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vrow[i] = vbase + (int64_t)(4 * g + i) * a.svs;
+    } else {
+      // Any page size: each token looks up its own page; tokens past the
+      // end are clamped to the last valid token (and masked below).
+      {
+        const int tk = min(t0 + r16, t_end - 1);
+        const int page = tk / a.ps;
+        const int phys = clamp_page(bt_row[(int64_t)page * a.sbp], a.num_pages);
+        krow = a.k + (int64_t)phys * a.skp + koff_h + (int64_t)(tk - page * a.ps) * a.sks;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tv = min(t0 + 4 * g + i, t_end - 1);
+        const int page = tv / a.ps;
+        const int phys = clamp_page(bt_row[(int64_t)page * a.sbp], a.num_pages);
+        vrow[i] = a.v + (int64_t)phys * a.svp + voff_h + (int64_t)(tv - page * a.ps) * a.svs;
+      }
+    }
+
+    h8_t kk[DK];
+#pragma unroll
+    for (int kp = 0; kp < DK; ++kp) kk[kp] = *reinterpret_cast<const h8_t*>(krow + kp * 32 + g * 8);
+    HVec<NDW> vv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vv[i] = load_hvec<NDW>(vrow[i] + r16 * DT);
+
+    // S^T[token 4g+i][row r16] over head_dim.
+    f4_t sacc = (f4_t)0.f;
+#pragma unroll
+    for (int kp = 0; kp < DK; ++kp) {
+      const h4_t k_lo = __builtin_shufflevector(kk[kp], kk[kp], 0, 1, 2, 3);
+      const h4_t k_hi = __builtin_shufflevector(kk[kp], kk[kp], 4, 5, 6, 7);
+      const h4_t q_lo = __builtin_shufflevector(qv[kp], qv[kp], 0, 1, 2, 3);
+      const h4_t q_hi = __builtin_shufflevector(qv[kp], qv[kp], 4, 5, 6, 7);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k_lo, q_lo, sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k_hi, q_hi, sacc, 0, 0, 0);
+    }
+
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = sacc[i] * a.scale_log2;
+    if (!full) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool valid = t0 + 4 * g + i < t_end;
+        x[i] = valid ? x[i] : kNegInf;
+        if (!valid) vv[i].zero();  // stale cache slots may hold NaN/Inf
+      }
+    }
+    float bm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    bm = fmaxf(bm, shfl_xor_f(bm, 16));
+    bm = fmaxf(bm, shfl_xor_f(bm, 32));
+    // Every block holds at least one valid token, so m_new is finite.
+    const float m_new = fmaxf(m_run, bm);
+    const float alpha = exp2_fast(m_run - m_new);
+    h4_t ph;
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const _Float16 p = (_Float16)exp2_fast(x[i] - m_new);
+      ph[i] = p;
+      psum += (float)p;  // l accumulates the same rounded weights P.V uses
+    }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      h4_t av;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = vv[i].h(dt);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, o[dt] * alpha, 0, 0, 0);
+    }
+  }
+
+  // Row totals: the four 16-lane groups hold disjoint token subsets.
+  float l_tot = l_run + shfl_xor_f(l_run, 16);
+  l_tot += shfl_xor_f(l_tot, 32);
+  if (row_ok) {
+    if (g == 0) sm_ml[wave * 16 + r16] = make_float2(m_run, l_tot);
+    // Lane owns O[row r16][g*D/4 + i*DT + dt].
+    float* dst = sm_o + (wave * a.gqa + r16) * D + g * (D / 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) dst[i * DT + dt] = o[dt][i];
+    }
+  }
+}
+
+// Engine 1: VALU dot products with DPP row reductions.
+template <int D, bool UNIFORM, int GQA_T>
+__device__ __forceinline__ void wave_loop_valu(const Phase1Args& a, int b, int kvh, int t_begin,
+                                               int t_end, int nblk, int wave, int nw, int lane,
+                                               float2* sm_ml, float* sm_o) {
+  constexpr int DT = D / 16;  // halves per lane per token
+  constexpr int NDW = DT / 2;
+  const int g = lane >> 4;    // token group: tokens 4g+i of each block
+  const int r16 = lane & 15;  // head_dim slice r16*DT .. +DT
+  const int gqa = a.gqa;
+
+  HVec<NDW> qh[GQA_T];
+#pragma unroll
+  for (int r = 0; r < GQA_T; ++r) {
+    if (r < gqa) {
+      const _Float16* qrow = a.q + (int64_t)b * a.sqb + (int64_t)(kvh * gqa + r) * a.sqh;
+      qh[r] = load_hvec<NDW>(qrow + r16 * DT);
+    } else {
+      qh[r].zero();
+    }
+  }
+  float m_run[GQA_T], l_run[GQA_T], acc[GQA_T][DT];
+#pragma unroll
+  for (int r = 0; r < GQA_T; ++r) {
+    m_run[r] = kNegInf;
+    l_run[r] = 0.f;
+#pragma unroll
+    for (int e = 0; e < DT; ++e) acc[r][e] = 0.f;
+  }
+
+  const int64_t koff_h = (int64_t)kvh * a.skh;
+  const int64_t voff_h = (int64_t)kvh * a.svh;
+  const int32_t* bt_row = a.bt + (int64_t)b * a.sbb;
+
+  for (int j = wave; j < nblk; j += nw) {
+    const int t0 = t_begin + j * kBlockTokens;
+    const _Float16* krow[4];
+    const _Float16* vrow[4];
+    if constexpr (UNIFORM) {
+      const int page = t0 / a.ps;
+      const int phys = clamp_page(__builtin_amdgcn_readfirstlane(bt_row[(int64_t)page * a.sbp]), a.num_pages);
+      const int slot0 = t0 - page * a.ps;
+      const _Float16* kbase = a.k + (int64_t)phys * a.skp + koff_h + (int64_t)slot0 * a.sks;
+      const _Float16* vbase = a.v + (int64_t)phys * a.svp + voff_h + (int64_t)slot0 * a.svs;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        krow[i] = kbase + (int64_t)(4 * g + i) * a.sks;
+        vrow[i] = vbase + (int64_t)(4 * g + i) * a.svs;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tv = min(t0 + 4 * g + i, t_end - 1);
+        const int page = tv / a.ps;
+        const int phys = clamp_page(bt_row[(int64_t)page * a.sbp], a.num_pages);
+        const int slot = tv - page * a.ps;
+        krow[i] = a.k + (int64_t)phys * a.skp + koff_h + (int64_t)slot * a.sks;
+        vrow[i] = a.v + (int64_t)phys * a.svp + voff_h + (int64_t)slot * a.svs;
+      }
+    }
+    HVec<NDW> kk[4], vv[4];
+    bool valid[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kk[i] = load_hvec<NDW>(krow[i] + r16 * DT);
+      vv[i] = load_hvec<NDW>(vrow[i] + r16 * DT);
+      valid[i] = t0 + 4 * g + i < t_end;
+      if (!valid[i]) vv[i].zero();
+    }
+    float vf[4][DT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int e = 0; e < DT; ++e) vf[i][e] = (float)vv[i].h(e);
+    }
+
+#pragma unroll
+    for (int r = 0; r < GQA_T; ++r) {
+      if (r >= gqa) break;
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float part = 0.f;
+#pragma unroll
+        for (int w = 0; w < NDW; ++w) part = __builtin_amdgcn_fdot2(qh[r].h2(w), kk[i].h2(w), part, false);
+        part = row16_sum(part);
+        sc[i] = valid[i] ? part * a.scale_log2 : kNegInf;
+      }
+      const float bm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      const float m_new = fmaxf(m_run[r], bm);
+      if (m_new == kNegInf) continue;  // this group has seen no valid token yet
+      const float alpha = exp2_fast(m_run[r] - m_new);
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = exp2_fast(sc[i] - m_new);
+      l_run[r] = l_run[r] * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+      for (int e = 0; e < DT; ++e) {
+        float t = acc[r][e] * alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t = fmaf(p[i], vf[i][e], t);
+        acc[r][e] = t;
+      }
+      m_run[r] = m_new;
+    }
+  }
+
+  // Merge the four token groups of this wave (lanes r16, r16+16, ...).
+#pragma unroll
+  for (int r = 0; r < GQA_T; ++r) {
+    if (r >= gqa) break;
+    float M = fmaxf(m_run[r], shfl_xor_f(m_run[r], 16));
+    M = fmaxf(M, shfl_xor_f(M, 32));
+    const float c = (m_run[r] == kNegInf) ? 0.f : exp2_fast(m_run[r] - M);
+    float l = l_run[r] * c;
+    l += shfl_xor_f(l, 16);
+    l += shfl_xor_f(l, 32);
+#pragma unroll
+    for (int e = 0; e < DT; ++e) {
+      float v = acc[r][e] * c;
+      v += shfl_xor_f(v, 16);
+      v += shfl_xor_f(v, 32);
+      acc[r][e] = v;
+    }
+    if (g == 0) {
+      if (r16 == 0) sm_ml[wave * 16 + r] = make_float2(M, l);
+      float* dst = sm_o + (wave * gqa + r) * D + r16 * DT;
+#pragma unroll
+      for (int e = 0; e < DT; ++e) dst[e] = acc[r][e];
+    }
+  }
+}
+
+// Phase 1: one workgroup per (split, kv head, sequence).
+template <int D, bool UNIFORM, int ENGINE, int GQA_T>
+__global__ __launch_bounds__(256) void pad_phase1_kernel(const Phase1Args a) {
+  extern __shared__ float4 smem_f4[];
+  float2* sm_ml = reinterpret_cast<float2*>(smem_f4);  // [nw][16]
+  const int nw = blockDim.x >> 6;
+  float* sm_o = reinterpret_cast<float*>(smem_f4) + nw * 32;  // [nw][gqa][D]
+
+  const int s = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+
+  const int L = max(a.sl[(int64_t)b * a.ssl], 0);
+  const int npages = min((L + a.ps - 1) / a.ps, a.max_pages);
+  const int p0 = s * a.pps;
+  if (!a.single && p0 >= npages) return;  // empty split: phase 2 never reads it
+  const int t_begin = p0 * a.ps;
+  const int t_end = min(min(p0 + a.pps, npages) * a.ps, L);
+  const int nblk = t_end > t_begin ? (t_end - t_begin + kBlockTokens - 1) / kBlockTokens : 0;
+
+  if constexpr (ENGINE == 0) {
+    wave_loop_mfma<D, UNIFORM>(a, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o);
+  } else {
+    wave_loop_valu<D, UNIFORM, GQA_T>(a, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o);
+  }
+  __syncthreads();
+
+  // Merge the waves' states: threads over (row, 4 consecutive d).
+  const int gqa = a.gqa;
+  const int total4 = gqa * (D / 4);
+  const int64_t part_row0 = (((int64_t)b * a.hkv + kvh) * a.num_splits + s) * gqa;
+  for (int e = threadIdx.x; e < total4; e += blockDim.x) {
+    const int row = e / (D / 4);
+    const int col = (e - row * (D / 4)) * 4;
+    float M = kNegInf;
+    for (int w = 0; w < nw; ++w) M = fmaxf(M, sm_ml[w * 16 + row].x);
+    f4_t acc = (f4_t)0.f;
+    float Ls = 0.f;
+    if (M != kNegInf) {
+      for (int w = 0; w < nw; ++w) {
+        const float2 ml = sm_ml[w * 16 + row];
+        const float c = (ml.x == kNegInf) ? 0.f : exp2_fast(ml.x - M);
+        Ls += c * ml.y;
+        acc += c * *reinterpret_cast<const f4_t*>(sm_o + (w * gqa + row) * D + col);
+      }
+    }
+    if (a.single) {
+      const float inv = Ls > 0.f ? 1.f / Ls : 0.f;  // seq_len == 0 -> zeros
+      h4_t hv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
+      *reinterpret_cast<h4_t*>(a.out + (int64_t)b * a.sob + (int64_t)(kvh * gqa + row) * a.soh + col) = hv;
+    } else {
+      *reinterpret_cast<f4_t*>(a.o_part + (part_row0 + row) * D + col) = acc;
+      if (col == 0) a.ml_part[part_row0 + row] = make_float2(M, Ls);
+    }
+  }
+}
+
+// Phase 2: one workgroup per (q head, sequence): LSE merge over splits.
+template <int D>
+__global__ __launch_bounds__(kPhase2Threads) void pad_phase2_kernel(const Phase2Args a) {
+  __shared__ float s_w[PAD_MAX_SPLITS];
+  __shared__ f4_t s_acc[kPhase2Threads];
+  __shared__ float s_red[kPhase2Threads / 64];
+  __shared__ float s_bcast;
+
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int kvh = h / a.gqa;
+  const int row = h - kvh * a.gqa;
+  _Float16* orow = a.out + (int64_t)b * a.sob + (int64_t)h * a.soh;
+
+  const int L = max(a.sl[(int64_t)b * a.ssl], 0);
+  const int npages = min((L + a.ps - 1) / a.ps, a.max_pages);
+  const int nsplit = min((npages + a.pps - 1) / a.pps, a.num_splits);
+  if (nsplit == 0) {  // seq_len == 0 -> zeros
+    for (int d = tid; d < D; d += kPhase2Threads) orow[d] = (_Float16)0.f;
+    return;
+  }
+  const int64_t base = (((int64_t)b * a.hkv + kvh) * a.num_splits) * a.gqa + row;
+  const int64_t sstride = a.gqa;
+
+  // Pass 1: global max of the split maxima.
+  float mx = kNegInf;
+  for (int s = tid; s < nsplit; s += kPhase2Threads) mx = fmaxf(mx, a.ml_part[base + s * sstride].x);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((tid & 63) == 0) s_red[tid >> 6] = mx;
+  __syncthreads();
+  if (tid == 0) {
+    float v = s_red[0];
+    for (int w = 1; w < kPhase2Threads / 64; ++w) v = fmaxf(v, s_red[w]);
+    s_bcast = v;
+  }
+  __syncthreads();
+  const float M = s_bcast;
+
+  // Pass 2: split weights and the total l.
+  float ls = 0.f;
+  for (int s = tid; s < nsplit; s += kPhase2Threads) {
+    const float2 ml = a.ml_part[base + s * sstride];
+    const float w = (ml.x == kNegInf) ? 0.f : exp2_fast(ml.x - M);
+    s_w[s] = w;
+    ls += w * ml.y;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off, 64);
+  __syncthreads();  // s_red reuse + s_w visible
+  if ((tid & 63) == 0) s_red[tid >> 6] = ls;
+  __syncthreads();
+  if (tid == 0) {
+    float v = 0.f;
+    for (int w = 0; w < kPhase2Threads / 64; ++w) v += s_red[w];
+    s_bcast = v;
+  }
+  __syncthreads();
+  const float Ltot = s_bcast;
+
+  // Pass 3: weighted sum of the partial outputs, float4 per thread.
+  constexpr int TPR = D / 4;                   // threads per split row
+  constexpr int SG = kPhase2Threads / TPR;     // split groups
+  const int sg = tid / TPR;
+  const int c4 = tid - sg * TPR;
+  f4_t acc = (f4_t)0.f;
+  if (sg < SG) {
+    for (int s = sg; s < nsplit; s += SG) {
+      const f4_t o = *reinterpret_cast<const f4_t*>(a.o_part + (base + s * sstride) * D + c4 * 4);
+      acc += s_w[s] * o;
+    }
+  }
+  s_acc[tid] = acc;
+  __syncthreads();
+  if (sg == 0) {
+    for (int g2 = 1; g2 < SG; ++g2) acc += s_acc[g2 * TPR + c4];
+    const float inv = Ltot > 0.f ? 1.f / Ltot : 0.f;
+    h4_t hv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
+    *reinterpret_cast<h4_t*>(orow + c4 * 4) = hv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+
+static bool head_dim_supported(int d) { return d == 32 || d == 64 || d == 96 || d == 128 || d == 256; }
+
+static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// VALU engine instantiations exist for these (head_dim, group) pairs.
+static bool valu_supported(int d, int gqa) { return (d == 64 || d == 128) && gqa <= 8; }
+
+static int merge_wave_cap(int gqa, int d) {
+  const int per_wave = 16 * 8 + gqa * d * 4;
+  int cap = kMergeLdsBudget / per_wave;
+  if (cap > kMaxWaves) cap = kMaxWaves;
+  if (cap < 1) cap = 1;
+  return cap;
+}
+
+static int validate_dims(const pad_decode_dims* d) {
+  if (!d) return PAD_ERR_NULL_POINTER;
+  if (d->batch < 0 || d->num_q_heads <= 0 || d->num_kv_heads <= 0 || d->head_dim <= 0 ||
+      d->page_size <= 0 || d->max_pages < 0 || d->num_pages < 0)
+    return PAD_ERR_INVALID_SHAPE;
+  if (!head_dim_supported(d->head_dim)) return PAD_ERR_UNSUPPORTED_HEAD_DIM;
+  if (d->num_q_heads % d->num_kv_heads != 0) return PAD_ERR_UNSUPPORTED_GQA;
+  if (d->num_q_heads / d->num_kv_heads > PAD_MAX_GQA) return PAD_ERR_UNSUPPORTED_GQA;
+  if (d->q_stride[2] != 1 || d->k_stride[3] != 1 || d->v_stride[3] != 1 || d->out_stride[2] != 1)
+    return PAD_ERR_STRIDE;
+  return PAD_OK;
+}
+
+static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int engine,
+                     pad_decode_plan_t* p) {
+  const int st = validate_dims(d);
+  if (st != PAD_OK) return st;
+  if (num_splits < 0 || num_splits > PAD_MAX_SPLITS) return PAD_ERR_NUM_SPLITS;
+  if (num_cus <= 0) num_cus = 256;
+  const int gqa = d->num_q_heads / d->num_kv_heads;
+  const int max_pages = d->max_pages > 0 ? d->max_pages : 1;
+  const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
+
+  int S;
+  int pps;
+  if (num_splits > 0) {
+    // Caller's split count, page-aligned: pages_per_split = ceil(max_pages/S).
+    // Splits past a sequence's last page are empty (never read).
+    S = num_splits;
+    pps = ceil_div(max_pages, S);
+  } else {
+    // Heuristic: enough workgroups to cover every CU a few times, but never
+    // fewer than kMinBlocks 16-token blocks per split, so the fp32 partial
+    // traffic (gqa*(D+2)*4 bytes per split) stays a small fraction of the
+    // split's K/V bytes (page_size*Hkv-share*D*4 per page).
+    const int kTargetGroups = 4 * num_cus;
+    const int kMinBlocks = 4;
+    const int64_t blocks_per_seq = ((int64_t)max_pages * d->page_size + kBlockTokens - 1) / kBlockTokens;
+    int64_t s_want = (kTargetGroups + units - 1) / units;
+    int64_t s_cap = blocks_per_seq / kMinBlocks;
+    if (s_cap < 1) s_cap = 1;
+    if (s_want > s_cap) s_want = s_cap;
+    if (s_want > PAD_MAX_SPLITS) s_want = PAD_MAX_SPLITS;
+    if (s_want < 1) s_want = 1;
+    pps = ceil_div(max_pages, s_want);
+    S = ceil_div(max_pages, pps);
+  }
+  const int64_t split_tokens = (int64_t)pps * d->page_size;
+  int nw = (int)((split_tokens + kBlockTokens - 1) / kBlockTokens);
+  const int cap = merge_wave_cap(gqa, d->head_dim);
+  if (nw > cap) nw = cap;
+  if (nw < 1) nw = 1;
+
+  p->num_splits = S;
+  p->pages_per_split = pps;
+  p->waves_per_group = nw;
+  p->single_pass = (S == 1) ? 1 : 0;
+  p->engine = engine;
+  p->reserved = 0;
+  p->workspace_bytes =
+      p->single_pass ? 0 : (size_t)d->batch * d->num_kv_heads * S * gqa * (size_t)(d->head_dim + 2) * 4 + 256;
+  return PAD_OK;
+}
+
+static int g_num_cus[64];
+
+static int device_cus(int* out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return PAD_ERR_DEVICE;
+  if (dev < 0 || dev >= 64) return PAD_ERR_DEVICE;
+  if (g_num_cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return PAD_ERR_DEVICE;
+    g_num_cus[dev] = n;
+  }
+  *out = g_num_cus[dev];
+  return PAD_OK;
+}
+
+template <int D, bool UNIFORM, int ENGINE, int GQA_T>
+static hipError_t launch_p1(const Phase1Args& a, dim3 grid, int nw, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((pad_phase1_kernel<D, UNIFORM, ENGINE, GQA_T>), grid, dim3(nw * 64), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int D, bool UNIFORM>
+static hipError_t dispatch_engine(const Phase1Args& a, dim3 grid, int nw, size_t lds, int engine,
+                                  hipStream_t st) {
+  if (engine == 1) {
+    if constexpr (D == 64 || D == 128) {
+      if (a.gqa == 1) return launch_p1<D, UNIFORM, 1, 1>(a, grid, nw, lds, st);
+      if (a.gqa == 2) return launch_p1<D, UNIFORM, 1, 2>(a, grid, nw, lds, st);
+      if (a.gqa <= 4) return launch_p1<D, UNIFORM, 1, 4>(a, grid, nw, lds, st);
+      if (a.gqa <= 6) return launch_p1<D, UNIFORM, 1, 6>(a, grid, nw, lds, st);
+      return launch_p1<D, UNIFORM, 1, 8>(a, grid, nw, lds, st);
+    }
+    return hipErrorInvalidValue;
+  }
+  return launch_p1<D, UNIFORM, 0, 0>(a, grid, nw, lds, st);
+}
+
+template <int D>
+static hipError_t dispatch_phase1(const Phase1Args& a, dim3 grid, int nw, size_t lds, int engine,
+                                  hipStream_t st) {
+  if (a.ps % kBlockTokens == 0) return dispatch_engine<D, true>(a, grid, nw, lds, engine, st);
+  return dispatch_engine<D, false>(a, grid, nw, lds, engine, st);
+}
+
+template <int D>
+static hipError_t launch_p2(const Phase2Args& a, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((pad_phase2_kernel<D>), grid, dim3(kPhase2Threads), 0, st, a);
+  return hipGetLastError();
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static int launch_impl(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
+                       void* out, void* ws, size_t ws_bytes, const pad_decode_dims* d, float scale,
+                       int num_splits, int engine, void* const* events, void* stream) {
+  if (engine != 0 && engine != 1) return PAD_ERR_INVALID_SHAPE;
+  int cus = 0;
+  int st = device_cus(&cus);
+  if (st != PAD_OK) return st;
+  pad_decode_plan_t plan;
+  st = plan_impl(d, num_splits, cus, engine, &plan);
+  if (st != PAD_OK) return st;
+  const int gqa = d->num_q_heads / d->num_kv_heads;
+  if (engine == 1 && !valu_supported(d->head_dim, gqa)) return PAD_ERR_UNSUPPORTED_GQA;
+  if (d->batch == 0) return PAD_OK;
+  if (!q || !k || !v || !bt || !sl || !out) return PAD_ERR_NULL_POINTER;
+  // 16-byte rows: every K/V/q/out row start must be 16-byte aligned.
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return PAD_ERR_ALIGNMENT;
+  if ((d->q_stride[0] | d->q_stride[1]) % 8 || (d->out_stride[0] | d->out_stride[1]) % 8 ||
+      (d->k_stride[0] | d->k_stride[1] | d->k_stride[2]) % 8 ||
+      (d->v_stride[0] | d->v_stride[1] | d->v_stride[2]) % 8)
+    return PAD_ERR_ALIGNMENT;
+  if (!plan.single_pass && (!ws || ws_bytes < plan.workspace_bytes)) return PAD_ERR_WORKSPACE;
+
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  const int S = plan.num_splits;
+  float* o_part = nullptr;
+  float2* ml_part = nullptr;
+  if (!plan.single_pass) {
+    uintptr_t base = ((uintptr_t)ws + 255u) & ~(uintptr_t)255u;
+    o_part = reinterpret_cast<float*>(base);
+    const size_t o_elems = (size_t)d->batch * d->num_kv_heads * S * gqa * d->head_dim;
+    ml_part = reinterpret_cast<float2*>(o_part + o_elems);
+  }
+
+  Phase1Args a;
+  a.q = static_cast<const _Float16*>(q);
+  a.k = static_cast<const _Float16*>(k);
+  a.v = static_cast<const _Float16*>(v);
+  a.bt = bt;
+  a.sl = sl;
+  a.out = static_cast<_Float16*>(out);
+  a.o_part = o_part;
+  a.ml_part = ml_part;
+  a.sqb = d->q_stride[0];
+  a.sqh = d->q_stride[1];
+  a.skp = d->k_stride[0];
+  a.sks = d->k_stride[1];
+  a.skh = d->k_stride[2];
+  a.svp = d->v_stride[0];
+  a.svs = d->v_stride[1];
+  a.svh = d->v_stride[2];
+  a.sbb = d->bt_stride[0];
+  a.sbp = d->bt_stride[1];
+  a.ssl = d->sl_stride;
+  a.sob = d->out_stride[0];
+  a.soh = d->out_stride[1];
+  a.num_pages = d->num_pages > 0 ? d->num_pages : 1;
+  a.gqa = gqa;
+  a.ps = d->page_size;
+  a.pps = plan.pages_per_split;
+  a.num_splits = S;
+  a.hkv = d->num_kv_heads;
+  a.max_pages = d->max_pages;
+  a.single = plan.single_pass;
+  a.scale_log2 = scale * kLog2e;
+
+  const int nw = plan.waves_per_group;
+  const size_t lds = (size_t)nw * 16 * sizeof(float2) + (size_t)nw * gqa * d->head_dim * sizeof(float);
+  const dim3 grid1(S, d->num_kv_heads, d->batch);
+
+  if (events && events[0] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[0]), hs) != hipSuccess)
+    return PAD_ERR_LAUNCH;
+  hipError_t e;
+  switch (d->head_dim) {
+    case 32: e = dispatch_phase1<32>(a, grid1, nw, lds, engine, hs); break;
+    case 64: e = dispatch_phase1<64>(a, grid1, nw, lds, engine, hs); break;
+    case 96: e = dispatch_phase1<96>(a, grid1, nw, lds, engine, hs); break;
+    case 128: e = dispatch_phase1<128>(a, grid1, nw, lds, engine, hs); break;
+    default: e = dispatch_phase1<256>(a, grid1, nw, lds, engine, hs); break;
+  }
+  if (e != hipSuccess) return PAD_ERR_LAUNCH;
+  if (events && events[1] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[1]), hs) != hipSuccess)
+    return PAD_ERR_LAUNCH;
+
+  if (!plan.single_pass) {
+    Phase2Args p2;
+    p2.o_part = o_part;
+    p2.ml_part = ml_part;
+    p2.sl = sl;
+    p2.out = a.out;
+    p2.ssl = a.ssl;
+    p2.sob = a.sob;
+    p2.soh = a.soh;
+    p2.gqa = gqa;
+    p2.ps = a.ps;
+    p2.pps = a.pps;
+    p2.num_splits = S;
+    p2.hkv = a.hkv;
+    p2.max_pages = a.max_pages;
+    const dim3 grid2(d->num_q_heads, d->batch);
+    switch (d->head_dim) {
+      case 32: e = launch_p2<32>(p2, grid2, hs); break;
+      case 64: e = launch_p2<64>(p2, grid2, hs); break;
+      case 96: e = launch_p2<96>(p2, grid2, hs); break;
+      case 128: e = launch_p2<128>(p2, grid2, hs); break;
+      default: e = launch_p2<256>(p2, grid2, hs); break;
+    }
+    if (e != hipSuccess) return PAD_ERR_LAUNCH;
+  }
+  if (events && events[2] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[2]), hs) != hipSuccess)
+    return PAD_ERR_LAUNCH;
+  return PAD_OK;
+}
+
+}  // namespace pad
+
+extern "C" {
+
+int pad_decode_plan(const pad_decode_dims* dims, int num_splits, int num_cus, pad_decode_plan_t* plan) {
+  if (!plan) return PAD_ERR_NULL_POINTER;
+  return pad::plan_impl(dims, num_splits, num_cus, 0, plan);
+}
+
+int pad_decode_workspace_bytes(const pad_decode_dims* dims, int num_splits, int num_cus, size_t* bytes) {
+  if (!bytes) return PAD_ERR_NULL_POINTER;
+  pad_decode_plan_t p;
+  const int st = pad::plan_impl(dims, num_splits, num_cus, 0, &p);
+  if (st != PAD_OK) return st;
+  *bytes = p.workspace_bytes;
+  return PAD_OK;
+}
+
+int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                      const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
+                      const pad_decode_dims* dims, float scale, int num_splits, void* stream) {
+  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, out, workspace, workspace_bytes, dims,
+                          scale, num_splits, 0, nullptr, stream);
+}
+
+int pad_decode_launch_ex(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                         const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
+                         const pad_decode_dims* dims, float scale, int num_splits, int engine,
+                         void* const* events, void* stream) {
+  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, out, workspace, workspace_bytes, dims,
+                          scale, num_splits, engine, events, stream);
+}
+
+int pad_device_num_cus(int* num_cus) {
+  if (!num_cus) return PAD_ERR_NULL_POINTER;
+  return pad::device_cus(num_cus);
+}
+
+const char* pad_status_string(int status) {
+  switch (status) {
+    case PAD_OK: return "ok";
+    case PAD_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case PAD_ERR_INVALID_SHAPE: return "invalid shape (non-positive or inconsistent sizes)";
+    case PAD_ERR_UNSUPPORTED_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 96, 128, 256)";
+    case PAD_ERR_UNSUPPORTED_GQA:
+      return "unsupported GQA group (num_q_heads must be a multiple of num_kv_heads, ratio <= 16)";
+    case PAD_ERR_STRIDE: return "head_dim must be contiguous (stride 1) for q, k_cache, v_cache and out";
+    case PAD_ERR_ALIGNMENT: return "q/k_cache/v_cache/out rows must be 16-byte aligned";
+    case PAD_ERR_WORKSPACE: return "workspace is NULL or smaller than pad_decode_workspace_bytes()";
+    case PAD_ERR_NUM_SPLITS: return "num_splits must be in [0, 1024]";
+    case PAD_ERR_LAUNCH: return "kernel launch failed";
+    case PAD_ERR_DEVICE: return "no usable HIP device";
+    default: return "unknown status";
+  }
+}
+
+int pad_decode_abi_version(void) { return PAD_ABI_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,147 @@
+// pa_torch.cpp - thin PyTorch-ROCm binding over the C ABI in pa_decode.h.
+//
+// Mirrors the reference's pybind11 module (cuda/binding.cpp:3-15), whose
+// `forward_v4` entry called paged_attn_decode_cuda_v4_launch
+// (cuda/kernel_v4_split_k.cu:205-268).  This file holds no kernels: it reads
+// shapes, strides and data pointers from the tensors, allocates the output
+// and the fp32 split workspace from PyTorch's caching allocator, and calls
+// pad_decode_launch_ex() on PyTorch's current HIP stream of q's device.
+// Argument errors surface as RuntimeError (the reference used TORCH_CHECK,
+// cuda/kernel_v4_split_k.cu:216-223).  No host synchronisation.
+
+#include <torch/extension.h>
+
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include "pa_decode.h"
+
+namespace {
+
+int cached_cus(int device) {
+  static int cus[64] = {0};
+  if (device < 0 || device >= 64) return 256;
+  if (cus[device] <= 0) {
+    int n = 0;
+    if (pad_device_num_cus(&n) != PAD_OK || n <= 0) n = 256;
+    cus[device] = n;
+  }
+  return cus[device];
+}
+
+void fill_dims(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+               const torch::Tensor& bt, const torch::Tensor& sl, const torch::Tensor& out,
+               pad_decode_dims* d) {
+  d->batch = static_cast<int32_t>(q.size(0));
+  d->num_q_heads = static_cast<int32_t>(q.size(1));
+  d->head_dim = static_cast<int32_t>(q.size(2));
+  d->num_pages = k.size(0);
+  d->page_size = static_cast<int32_t>(k.size(1));
+  d->num_kv_heads = static_cast<int32_t>(k.size(2));
+  d->max_pages = static_cast<int32_t>(bt.size(1));
+  for (int i = 0; i < 3; ++i) d->q_stride[i] = q.stride(i);
+  for (int i = 0; i < 4; ++i) {
+    d->k_stride[i] = k.stride(i);
+    d->v_stride[i] = v.stride(i);
+  }
+  d->bt_stride[0] = bt.stride(0);
+  d->bt_stride[1] = bt.stride(1);
+  d->sl_stride = sl.stride(0);
+  for (int i = 0; i < 3; ++i) d->out_stride[i] = out.stride(i);
+}
+
+torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                      torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                      int64_t num_splits, int64_t engine) {
+  TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && block_table.is_cuda() &&
+                  seq_lens.is_cuda(),
+              "pa_decode: all tensors must be on the GPU");
+  TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() &&
+                  q.device() == block_table.device() && q.device() == seq_lens.device(),
+              "pa_decode: all tensors must be on the same device");
+  TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
+                  v_cache.scalar_type() == at::kHalf,
+              "pa_decode: q, k_cache and v_cache must be float16");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt && seq_lens.scalar_type() == at::kInt,
+              "pa_decode: block_table and seq_lens must be int32");
+  TORCH_CHECK(q.dim() == 3, "pa_decode: q must be [batch, num_q_heads, head_dim]");
+  TORCH_CHECK(k_cache.dim() == 4, "pa_decode: k_cache must be [num_pages, page_size, num_kv_heads, head_dim]");
+  TORCH_CHECK(v_cache.sizes() == k_cache.sizes(), "pa_decode: v_cache shape must match k_cache");
+  TORCH_CHECK(block_table.dim() == 2 && block_table.size(0) == q.size(0),
+              "pa_decode: block_table must be [batch, max_pages]");
+  TORCH_CHECK(seq_lens.dim() == 1 && seq_lens.size(0) == q.size(0), "pa_decode: seq_lens must be [batch]");
+  TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
+
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+  pad_decode_dims d;
+  fill_dims(q, k_cache, v_cache, block_table, seq_lens, out, &d);
+
+  const int cus = cached_cus(q.get_device());
+  size_t ws_bytes = 0;
+  int st = pad_decode_workspace_bytes(&d, static_cast<int>(num_splits), cus, &ws_bytes);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  torch::Tensor ws;
+  void* ws_ptr = nullptr;
+  if (ws_bytes > 0) {
+    ws = torch::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
+    ws_ptr = ws.data_ptr();
+  }
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  st = pad_decode_launch_ex(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                            block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
+                            ws_ptr, ws_bytes, &d, static_cast<float>(scale), static_cast<int>(num_splits),
+                            static_cast<int>(engine), nullptr, stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return out;
+}
+
+// Same argument list as the reference's forward_v4 binding
+// (cuda/kernels.h:60-70): gqa_ratio, head_dim and page_size must agree with
+// the tensor shapes.
+torch::Tensor forward_v4(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                         torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                         int64_t gqa_ratio, int64_t head_dim, int64_t page_size, int64_t num_splits) {
+  TORCH_CHECK(q.dim() == 3 && k_cache.dim() == 4, "pa_decode: bad tensor ranks");
+  TORCH_CHECK(gqa_ratio >= 1 && gqa_ratio <= PAD_MAX_GQA,
+              "pa_decode: gqa_ratio (", gqa_ratio, ") must be in [1, ", PAD_MAX_GQA, "]");
+  TORCH_CHECK(q.size(1) == gqa_ratio * k_cache.size(2), "pa_decode: gqa_ratio does not match the head counts");
+  TORCH_CHECK(head_dim == q.size(2), "pa_decode: head_dim does not match q");
+  TORCH_CHECK(page_size == k_cache.size(1), "pa_decode: page_size does not match k_cache");
+  TORCH_CHECK(num_splits >= 1, "pa_decode: num_splits must be >= 1");
+  return forward(q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, 0);
+}
+
+// The plan the launch would use, as a dict (host only).
+py::dict plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+              int64_t page_size, int64_t max_pages, int64_t num_splits, int64_t num_cus) {
+  pad_decode_dims d;
+  std::memset(&d, 0, sizeof(d));
+  d.batch = static_cast<int32_t>(batch);
+  d.num_q_heads = static_cast<int32_t>(num_q_heads);
+  d.num_kv_heads = static_cast<int32_t>(num_kv_heads);
+  d.head_dim = static_cast<int32_t>(head_dim);
+  d.page_size = static_cast<int32_t>(page_size);
+  d.max_pages = static_cast<int32_t>(max_pages);
+  d.q_stride[2] = d.k_stride[3] = d.v_stride[3] = d.out_stride[2] = 1;
+  pad_decode_plan_t p;
+  const int st = pad_decode_plan(&d, static_cast<int>(num_splits), static_cast<int>(num_cus), &p);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  py::dict r;
+  r["num_splits"] = p.num_splits;
+  r["pages_per_split"] = p.pages_per_split;
+  r["waves_per_group"] = p.waves_per_group;
+  r["single_pass"] = p.single_pass;
+  r["workspace_bytes"] = p.workspace_bytes;
+  return r;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("forward", &forward, "Paged-attention decode (q, k_cache, v_cache, block_table, seq_lens, scale, "
+                             "num_splits, engine) -> out");
+  m.def("forward_v4", &forward_v4, "Paged-attention decode with the reference forward_v4 argument list");
+  m.def("plan", &plan, "Split plan for the given shapes (host only)");
+  m.def("abi_version", &pad_decode_abi_version, "C ABI version of the linked libpa_decode.so");
+}

@@ -1,0 +1,64 @@
+"""Split-count heuristic, mirrored in Python.
+
+The launch uses the C++ implementation (``plan_impl`` in csrc/pa_decode.hip,
+exposed as ``pad_decode_plan``); this module restates it so the choice can be
+inspected and unit-tested on a host without a GPU, and the tests check that
+both agree.  It replaces the reference's constant default
+``_DEFAULT_NUM_SPLITS = 64`` (src/kernel_cuda_v4.py:16), which over-splits
+large batches (profiles/notes.md:875-883 of the reference).
+
+Inputs are shapes only (no ``seq_lens`` read, so no device sync):
+batch, kv heads, head_dim, page_size, ``max_pages = block_table.shape[1]``
+and the CU count.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+BLOCK_TOKENS = 16          # tokens per wave iteration (one MFMA tile)
+MAX_WAVES = 4              # waves per phase-1 workgroup
+MAX_SPLITS = 1024          # PAD_MAX_SPLITS
+MERGE_LDS_BUDGET = 48 * 1024
+TARGET_GROUPS_PER_CU = 4   # phase-1 workgroups per CU the heuristic aims at
+MIN_BLOCKS_PER_SPLIT = 4   # never split below this many 16-token blocks
+
+
+@dataclass(frozen=True)
+class Plan:
+    num_splits: int
+    pages_per_split: int
+    waves_per_group: int
+    single_pass: bool
+    workspace_bytes: int
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int, max_pages: int,
+         num_splits: int = 0, num_cus: int = 256) -> Plan:
+    """Same result as ``pad_decode_plan`` for valid arguments."""
+    if num_cus <= 0:
+        num_cus = 256
+    gqa = num_q_heads // num_kv_heads
+    mp = max_pages if max_pages > 0 else 1
+    units = max(batch, 1) * num_kv_heads
+    if num_splits > 0:
+        s = num_splits
+        pps = _cdiv(mp, s)
+    else:
+        blocks_per_seq = _cdiv(mp * page_size, BLOCK_TOKENS)
+        want = _cdiv(TARGET_GROUPS_PER_CU * num_cus, units)
+        cap = max(blocks_per_seq // MIN_BLOCKS_PER_SPLIT, 1)
+        want = max(min(want, cap, MAX_SPLITS), 1)
+        pps = _cdiv(mp, want)
+        s = _cdiv(mp, pps)
+    nw = _cdiv(pps * page_size, BLOCK_TOKENS)
+    per_wave = 16 * 8 + gqa * head_dim * 4
+    cap_w = max(min(MERGE_LDS_BUDGET // per_wave, MAX_WAVES), 1)
+    nw = max(min(nw, cap_w), 1)
+    single = s == 1
+    ws = 0 if single else batch * num_kv_heads * s * gqa * (head_dim + 2) * 4 + 256
+    return Plan(s, pps, nw, single, ws)

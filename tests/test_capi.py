@@ -1,0 +1,223 @@
+"""The C ABI of libpa_decode.so (include/pa_decode.h).
+
+CPU tests: the library loads, exports every function the header declares,
+and its host-only functions (plan, workspace size, status strings) behave;
+the plan agrees with the Python mirror in heuristics.py.  GPU tests call
+pad_decode_launch / pad_decode_launch_ex through ctypes with raw device
+pointers, a caller-owned workspace and stream, and check parity.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from paged_attention_decode_amd import _native, heuristics
+from tests.helpers import assert_parity, make_cache, shuffled_table
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "pa_decode.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(pad_\w+)\s*\(", text, flags=re.M)))
+
+
+def _dims(batch=4, hq=12, hkv=2, d=128, ps=16, max_pages=256, num_pages=1024):
+    dm = _native.PadDims()
+    dm.batch, dm.num_q_heads, dm.num_kv_heads, dm.head_dim = batch, hq, hkv, d
+    dm.page_size, dm.max_pages, dm.num_pages = ps, max_pages, num_pages
+    for i, s in enumerate((hq * d, d, 1)):
+        dm.q_stride[i] = s
+        dm.out_stride[i] = s
+    for i, s in enumerate((ps * hkv * d, hkv * d, d, 1)):
+        dm.k_stride[i] = s
+        dm.v_stride[i] = s
+    dm.bt_stride[0], dm.bt_stride[1] = max_pages, 1
+    dm.sl_stride = 1
+    return dm
+
+
+def test_header_declares_the_expected_entry_points():
+    assert _declared_functions() == sorted(_native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.capi()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.pad_decode_abi_version() == 1
+
+
+def test_status_strings():
+    lib = _native.capi()
+    assert lib.pad_status_string(0) == b"ok"
+    for code in range(1, 11):
+        assert lib.pad_status_string(code) not in (b"ok", b"unknown status")
+    assert lib.pad_status_string(999) == b"unknown status"
+
+
+@pytest.mark.parametrize("batch,hq,hkv,d,ps,max_pages,splits,cus", [
+    (1, 12, 2, 128, 16, 256, 0, 256),
+    (16, 12, 2, 128, 16, 256, 0, 256),
+    (64, 12, 2, 128, 16, 256, 0, 256),
+    (32, 12, 2, 128, 32, 256, 0, 256),
+    (1, 32, 8, 128, 16, 8192, 0, 256),
+    (256, 64, 8, 128, 16, 2048, 0, 256),
+    (1, 12, 2, 128, 16, 64, 0, 256),
+    (3, 12, 2, 128, 16, 250, 8, 256),
+    (1, 12, 2, 128, 16, 1, 8, 256),
+    (2, 32, 2, 256, 16, 40, 0, 80),
+    (5, 16, 1, 96, 1, 100, 0, 0),
+])
+def test_plan_matches_python_mirror(batch, hq, hkv, d, ps, max_pages, splits, cus):
+    lib = _native.capi()
+    p = _native.PadPlan()
+    assert lib.pad_decode_plan(ctypes.byref(_dims(batch, hq, hkv, d, ps, max_pages)), splits, cus, ctypes.byref(p)) == 0
+    m = heuristics.plan(batch, hq, hkv, d, ps, max_pages, splits, cus)
+    assert (p.num_splits, p.pages_per_split, p.waves_per_group, bool(p.single_pass), p.workspace_bytes) == (
+        m.num_splits, m.pages_per_split, m.waves_per_group, m.single_pass, m.workspace_bytes)
+    ws = ctypes.c_size_t()
+    assert lib.pad_decode_workspace_bytes(ctypes.byref(_dims(batch, hq, hkv, d, ps, max_pages)), splits, cus,
+                                          ctypes.byref(ws)) == 0
+    assert ws.value == m.workspace_bytes
+
+
+def test_heuristic_properties():
+    # Fills the chip at batch 1 without splitting below 4 blocks per split,
+    # and does not over-split large batches.
+    p1 = heuristics.plan(1, 12, 2, 128, 16, 256)
+    assert p1.num_splits * 2 >= 64 and p1.pages_per_split * 16 >= 64
+    p64 = heuristics.plan(64, 12, 2, 128, 16, 256)
+    assert p64.num_splits <= 8
+    p_big = heuristics.plan(256, 64, 8, 128, 16, 2048)
+    assert p_big.num_splits == 1 and p_big.single_pass
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("head_dim", 48, 3),
+    ("head_dim", 512, 3),
+    ("num_q_heads", 13, 4),
+    ("num_q_heads", 34, 4),
+    ("num_kv_heads", 0, 2),
+    ("page_size", 0, 2),
+    ("batch", -1, 2),
+])
+def test_plan_rejects_bad_shapes(field, value, code):
+    lib = _native.capi()
+    dm = _dims()
+    setattr(dm, field, value)
+    p = _native.PadPlan()
+    assert lib.pad_decode_plan(ctypes.byref(dm), 0, 256, ctypes.byref(p)) == code
+
+
+def test_plan_rejects_bad_strides_and_splits():
+    lib = _native.capi()
+    p = _native.PadPlan()
+    dm = _dims()
+    dm.k_stride[3] = 2
+    assert lib.pad_decode_plan(ctypes.byref(dm), 0, 256, ctypes.byref(p)) == 5
+    assert lib.pad_decode_plan(ctypes.byref(_dims()), -1, 256, ctypes.byref(p)) == 8
+    assert lib.pad_decode_plan(ctypes.byref(_dims()), 1025, 256, ctypes.byref(p)) == 8
+    assert lib.pad_decode_plan(None, 0, 256, ctypes.byref(p)) == 1
+
+
+# --------------------------------------------------------------------- GPU ---
+
+def _launch(lib, q, k, v, bt, sl, out, ws, dm, scale, splits, engine=None, stream=None, events=None):
+    wsp = ws.data_ptr() if ws is not None else None
+    wsb = ws.numel() if ws is not None else 0
+    if engine is None:
+        return lib.pad_decode_launch(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+                                     out.data_ptr(), wsp, wsb, ctypes.byref(dm), scale, splits, stream)
+    return lib.pad_decode_launch_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+                                    out.data_ptr(), wsp, wsb, ctypes.byref(dm), scale, splits, engine, events, stream)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("splits", [0, 1, 6])
+def test_launch_through_c_abi(splits):
+    from oracle.reference import decode_fp16_protocol
+
+    lib = _native.capi()
+    lens = [1, 77, 400, 1000]
+    bt, n = shuffled_table(lens, 16, spare_pages=3, extra_cols=1, seed=3)
+    k, v = make_cache(n, 16, 2, 128, seed=3)
+    q = torch.randn(4, 12, 128, generator=torch.Generator().manual_seed(3))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    expected = decode_fp16_protocol(q, k, v, bt, sl)
+    qd, kd, vd = q.half().cuda(), k.half().cuda(), v.half().cuda()
+    btd, sld = bt.cuda(), sl.cuda()
+    out = torch.empty_like(qd)
+    dm = _native.dims_for(qd, kd, vd, btd, sld, out)
+    wsb = ctypes.c_size_t()
+    assert lib.pad_decode_workspace_bytes(ctypes.byref(dm), splits, 0, ctypes.byref(wsb)) == 0
+    ws = torch.empty(max(wsb.value, 1), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    st = _launch(lib, qd, kd, vd, btd, sld, out, ws, dm, 1.0 / 128 ** 0.5, splits, stream=stream.cuda_stream)
+    assert st == 0, lib.pad_status_string(st)
+    stream.synchronize()
+    assert_parity(out, expected)
+
+
+@pytest.mark.gpu
+def test_launch_ex_events_and_engines():
+    from oracle.reference import decode_fp16_protocol
+
+    lib = _native.capi()
+    lens = [300, 2000]
+    bt, n = shuffled_table(lens, 16, spare_pages=2, extra_cols=0, seed=4)
+    k, v = make_cache(n, 16, 2, 128, seed=4)
+    q = torch.randn(2, 12, 128, generator=torch.Generator().manual_seed(4))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    expected = decode_fp16_protocol(q, k, v, bt, sl)
+    qd, kd, vd, btd, sld = q.half().cuda(), k.half().cuda(), v.half().cuda(), bt.cuda(), sl.cuda()
+    for engine in (0, 1):
+        out = torch.empty_like(qd)
+        dm = _native.dims_for(qd, kd, vd, btd, sld, out)
+        ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        arr = (ctypes.c_void_p * 3)(*[e.cuda_event for e in evs])
+        for e in evs:  # events must exist on the device before the library records them
+            e.record()
+        torch.cuda.synchronize()
+        st = _launch(lib, qd, kd, vd, btd, sld, out, ws, dm, 1.0 / 128 ** 0.5, 4, engine=engine,
+                     stream=torch.cuda.current_stream().cuda_stream, events=arr)
+        assert st == 0, lib.pad_status_string(st)
+        torch.cuda.synchronize()
+        assert evs[0].elapsed_time(evs[1]) > 0.0
+        assert evs[0].elapsed_time(evs[2]) >= evs[0].elapsed_time(evs[1])
+        assert_parity(out, expected)
+
+
+@pytest.mark.gpu
+def test_launch_rejects_bad_arguments_without_launching():
+    lib = _native.capi()
+    q = torch.zeros(1, 12, 128, dtype=torch.float16, device="cuda")
+    k = torch.zeros(4, 16, 2, 128, dtype=torch.float16, device="cuda")
+    bt = torch.zeros(1, 4, dtype=torch.int32, device="cuda")
+    sl = torch.full((1,), 40, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    dm = _native.dims_for(q, k, k, bt, sl, out)
+    # Workspace missing for a split launch.
+    assert _launch(lib, q, k, k, bt, sl, out, None, dm, 0.1, 4) == 7
+    # Misaligned output row.
+    flat = torch.empty(12 * 128 + 8, dtype=torch.float16, device="cuda")
+    bad_out = flat[1:1 + 12 * 128].view(1, 12, 128)
+    assert lib.pad_decode_launch(q.data_ptr(), k.data_ptr(), k.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+                                 bad_out.data_ptr(), None, 0, ctypes.byref(dm), 0.1, 1, None) == 6
+    # Null pointer.
+    assert lib.pad_decode_launch(None, k.data_ptr(), k.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+                                 out.data_ptr(), None, 0, ctypes.byref(dm), 0.1, 1, None) == 1
+    # VALU engine does not cover a group of 16.
+    q16 = torch.zeros(1, 32, 128, dtype=torch.float16, device="cuda")
+    dm16 = _native.dims_for(q16, k, k, bt, sl, torch.empty_like(q16))
+    assert lib.pad_decode_launch_ex(q16.data_ptr(), k.data_ptr(), k.data_ptr(), bt.data_ptr(), sl.data_ptr(),
+                                    q16.data_ptr(), None, 0, ctypes.byref(dm16), 0.1, 1, 1, None, None) == 4
+    torch.cuda.synchronize()

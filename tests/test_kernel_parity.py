@@ -1,0 +1,265 @@
+"""GPU parity of the HIP decode path against the CPU oracle.
+
+Mirrors the reference's tests/test_kernel_cuda_v4.py (primary shape :36-59,
+split invariance :62-76, num_splits=1 anchor :79-111, oversplit :114-127,
+partial page :130-141, GQA ratios :144-155, ragged :158-178, fuzz :181-190)
+for both phase-1 engines, with the fp16-rounding protocol of
+tests/kernel_test_utils.py:47-51 (the oracle sees the same fp16 inputs).
+
+Tolerance: atol = rtol = 2e-3 against the fp32 oracle (the contract), and the
+reference's own rtol 1e-2 / atol 1e-3 (assert_parity checks both).
+"""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+
+from oracle.reference import decode_fp16_protocol
+from tests.helpers import (
+    assert_parity,
+    cdiv,
+    contiguous_table,
+    make_cache,
+    random_case,
+    shuffled_table,
+)
+
+pytestmark = pytest.mark.gpu
+
+FUZZ = int(os.environ.get("PAD_KERNEL_FUZZ_ITERS", "20"))
+ENGINES = [0, 1]
+
+
+def _run(q, k, v, bt, sl, engine=0, **kw):
+    import paged_attention_decode_amd as pad
+
+    dev = "cuda"
+    return pad.paged_attention_decode_ex(q.half().to(dev), k.half().to(dev), v.half().to(dev), bt.to(dev),
+                                         sl.to(dev), engine=engine, **kw)
+
+
+def _check(q, k, v, bt, sl, engine=0, num_splits=None, scale=None):
+    expected = decode_fp16_protocol(q, k, v, bt, sl, scale)
+    actual = _run(q, k, v, bt, sl, engine=engine, num_splits=num_splits, scale=scale)
+    assert actual.dtype == torch.float16 and actual.shape == q.shape
+    assert_parity(actual, expected)
+    return actual
+
+
+def _engine_ok(engine, group, d):
+    return engine == 0 or (d in (64, 128) and group <= 8)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+@pytest.mark.parametrize("num_splits", [None, 1, 8])
+def test_primary_target_shape(engine, num_splits):
+    lens = [1, 17, 256, 4000]
+    bt, total = contiguous_table(lens, 16, extra_cols=0)
+    k, v = make_cache(total + 3, 16, 2, 128, seed=0)
+    q = torch.randn(4, 12, 128, generator=torch.Generator().manual_seed(0))
+    _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), engine, num_splits)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+@pytest.mark.parametrize("num_splits", [1, 2, 4, 8, 16, 64, 125, 200])
+def test_split_invariance(engine, num_splits):
+    seq, ps = 2000, 16
+    n = cdiv(seq, ps)
+    k, v = make_cache(n, ps, 2, 128, seed=600 + num_splits)
+    q = torch.randn(1, 12, 128, generator=torch.Generator().manual_seed(num_splits))
+    _check(q, k, v, torch.arange(n, dtype=torch.int32)[None], torch.tensor([seq], dtype=torch.int32), engine,
+           num_splits)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_split_counts_agree_tightly(engine):
+    # num_splits=1 (single pass, phase 1 normalises) is the unsplit anchor
+    # (analysis/split_k_derivation.md:88-99); every split count must agree
+    # with it far inside the oracle tolerance.
+    lens = [1, 17, 4000]
+    bt, total = contiguous_table(lens, 16)
+    k, v = make_cache(total + 3, 16, 2, 128, seed=42)
+    q = torch.randn(3, 12, 128, generator=torch.Generator().manual_seed(42))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    base = _run(q, k, v, bt, sl, engine, num_splits=1).float()
+    for s in (2, 3, 7, 16, 64, 250):
+        other = _run(q, k, v, bt, sl, engine, num_splits=s).float()
+        torch.testing.assert_close(other, base, rtol=2e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_oversplit_more_splits_than_tokens(engine):
+    k, v = make_cache(1, 16, 2, 128, seed=700)
+    q = torch.randn(1, 12, 128, generator=torch.Generator().manual_seed(700))
+    _check(q, k, v, torch.zeros(1, 1, dtype=torch.int32), torch.tensor([5], dtype=torch.int32), engine, 8)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_partial_last_page(engine):
+    seq, ps = 100, 16
+    n = cdiv(seq, ps)
+    k, v = make_cache(n, ps, 2, 128, seed=1)
+    q = torch.randn(1, 12, 128, generator=torch.Generator().manual_seed(1))
+    _check(q, k, v, torch.arange(n, dtype=torch.int32)[None], torch.tensor([seq], dtype=torch.int32), engine)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+@pytest.mark.parametrize("group", [1, 2, 4, 6, 8, 16])
+def test_gqa_ratios(engine, group):
+    if not _engine_ok(engine, group, 128):
+        pytest.skip("VALU engine covers groups <= 8")
+    seq, ps = 200, 16
+    n = cdiv(seq, ps)
+    k, v = make_cache(n, ps, 2, 128, seed=100 + group)
+    q = torch.randn(1, 2 * group, 128, generator=torch.Generator().manual_seed(group))
+    _check(q, k, v, torch.arange(n, dtype=torch.int32)[None], torch.tensor([seq], dtype=torch.int32), engine)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_ragged_batch_and_row_isolation(engine):
+    lens = [3, 17, 100, 512]
+    bt, total = contiguous_table(lens, 16)
+    k, v = make_cache(total + 3, 16, 2, 128, seed=43)
+    q = torch.randn(4, 12, 128, generator=torch.Generator().manual_seed(43))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    batched = _check(q, k, v, bt, sl, engine)
+    for b in range(4):
+        solo = _run(q[b:b + 1], k, v, bt[b:b + 1], sl[b:b + 1], engine)
+        torch.testing.assert_close(solo.float(), batched[b:b + 1].float(), rtol=2e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_zero_length_rows_give_zeros(engine):
+    lens = [0, 20, 0, 33]
+    bt, n = shuffled_table(lens, 16, spare_pages=2, extra_cols=1, seed=5)
+    k, v = make_cache(n, 16, 2, 128, seed=5)
+    q = torch.randn(4, 8, 128, generator=torch.Generator().manual_seed(5))
+    for s in (None, 1, 4):
+        out = _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), engine, s)
+        assert torch.all(out[0] == 0) and torch.all(out[2] == 0)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_poisoned_holes_and_nan_slots(engine):
+    # Unused columns/pages and the unused tail slots of the last page hold
+    # NaN: a kernel that reads or weights any of them produces NaN.
+    lens = [37, 5]
+    bt, n = shuffled_table(lens, 16, spare_pages=3, extra_cols=2, seed=9)
+    k, v = make_cache(n, 16, 2, 128, seed=9)
+    used = {int(bt[0, j]) for j in range(3)} | {int(bt[1, 0])}
+    for p in range(n):
+        if p not in used:
+            k[p] = float("nan")
+            v[p] = float("nan")
+    last0, last1 = int(bt[0, 2]), int(bt[1, 0])
+    k[last0, 5:] = float("nan")
+    v[last0, 5:] = float("nan")
+    k[last1, 5:] = float("nan")
+    v[last1, 5:] = float("nan")
+    q = torch.randn(2, 12, 128, generator=torch.Generator().manual_seed(9))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    k_clean, v_clean = torch.nan_to_num(k), torch.nan_to_num(v)
+    expected = decode_fp16_protocol(q, k_clean, v_clean, bt, sl)
+    for s in (None, 1, 2):
+        assert_parity(_run(q, k, v, bt, sl, engine, num_splits=s), expected)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+@pytest.mark.parametrize("ps", [1, 4, 8, 12, 16, 32, 64])
+def test_page_sizes(engine, ps):
+    lens = [1, ps + 3, 150, 77]
+    bt, n = shuffled_table(lens, ps, spare_pages=2, extra_cols=1, seed=ps)
+    k, v = make_cache(n, ps, 2, 128, seed=ps)
+    q = torch.randn(4, 12, 128, generator=torch.Generator().manual_seed(ps))
+    for s in (None, 3):
+        _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), engine, s)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+@pytest.mark.parametrize("d", [32, 64, 96, 128, 256])
+def test_head_dims(engine, d):
+    if not _engine_ok(engine, 4, d):
+        pytest.skip("VALU engine covers head_dim 64/128")
+    lens = [9, 130, 300]
+    bt, n = shuffled_table(lens, 16, spare_pages=2, extra_cols=1, seed=d)
+    k, v = make_cache(n, 16, 2, d, seed=d)
+    q = torch.randn(3, 8, d, generator=torch.Generator().manual_seed(d))
+    for s in (None, 1, 5):
+        _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), engine, s)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_scaled_keys_stress_softmax_range(engine):
+    lens = [300, 64]
+    bt, n = shuffled_table(lens, 16, spare_pages=1, extra_cols=0, seed=21)
+    k, v = make_cache(n, 16, 2, 128, seed=21)
+    g = torch.Generator().manual_seed(21)
+    for _ in range(6):
+        p, s = int(torch.randint(0, n, (1,), generator=g)), int(torch.randint(0, 16, (1,), generator=g))
+        k[p, s] *= 8.0
+    q = torch.randn(2, 12, 128, generator=g)
+    for s in (None, 1, 8):
+        _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), engine, s)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_explicit_scale_and_int64_indices(engine):
+    lens = [50, 200]
+    bt, n = shuffled_table(lens, 16, spare_pages=2, extra_cols=0, seed=31)
+    k, v = make_cache(n, 16, 2, 128, seed=31)
+    q = torch.randn(2, 12, 128, generator=torch.Generator().manual_seed(31))
+    _check(q, k, v, bt.long(), torch.tensor(lens, dtype=torch.int64), engine, None, scale=0.05)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+def test_strided_inputs(engine):
+    # q as a slice of a wider tensor; caches as views of a bigger buffer with
+    # padded strides (the reference passes all strides, cuda/kernel_v4_split_k.cu:248-254).
+    import paged_attention_decode_amd as pad
+
+    lens = [40, 90]
+    bt, n = shuffled_table(lens, 16, spare_pages=1, extra_cols=0, seed=41)
+    k, v = make_cache(n, 16, 2, 128, seed=41)
+    q = torch.randn(2, 12, 128, generator=torch.Generator().manual_seed(41))
+    expected = decode_fp16_protocol(q, k, v, bt, torch.tensor(lens, dtype=torch.int32))
+    qw = torch.zeros(2, 12, 256, dtype=torch.float16, device="cuda")
+    qw[:, :, 64:192] = q.half().cuda()
+    kw = torch.zeros(n, 16, 3, 136, dtype=torch.float16, device="cuda")
+    vw = torch.zeros(n, 16, 3, 136, dtype=torch.float16, device="cuda")
+    kw[:, :, :2, :128] = k.half().cuda()
+    vw[:, :, :2, :128] = v.half().cuda()
+    out = pad.paged_attention_decode_ex(qw[:, :, 64:192], kw[:, :, :2, :128], vw[:, :, :2, :128], bt.cuda(),
+                                        torch.tensor(lens, dtype=torch.int32).cuda(), engine=engine)
+    assert_parity(out, expected)
+
+
+def test_runs_on_current_stream():
+    import paged_attention_decode_amd as pad
+
+    lens = [500, 1000]
+    bt, n = shuffled_table(lens, 16, spare_pages=1, extra_cols=0, seed=51)
+    k, v = make_cache(n, 16, 2, 128, seed=51)
+    q = torch.randn(2, 12, 128, generator=torch.Generator().manual_seed(51))
+    expected = decode_fp16_protocol(q, k, v, bt, torch.tensor(lens, dtype=torch.int32))
+    args = [q.half().cuda(), k.half().cuda(), v.half().cuda(), bt.cuda(), torch.tensor(lens, dtype=torch.int32).cuda()]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        outs = [pad.paged_attention_decode(*args) for _ in range(3)]
+    s.synchronize()
+    for o in outs:
+        assert_parity(o, expected)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
+@pytest.mark.parametrize("seed", range(FUZZ))
+def test_fuzz_shape_matrix(engine, seed):
+    q, k, v, bt, sl = random_case(seed, gqa=(1, 2, 4, 6, 8), head_dims=(32, 64, 128), page_sizes=(1, 8, 16, 32),
+                                  min_len=0, max_len=300)
+    if not _engine_ok(engine, q.shape[1] // k.shape[2], q.shape[2]):
+        pytest.skip("shape outside the VALU engine")
+    for s in (None, 4):
+        _check(q, k, v, bt, sl, engine, s)
