@@ -1,0 +1,261 @@
+"""Benchmark of the MI355X paged-attention decode path.
+
+Metric: µs per decode call and achieved HBM GB/s (% of the
+8 TB/s peak) on the GQA 12/2, head_dim 128, page 16 shape at batch 1-64,
+seq_len 4096 (configuration C2).
+
+What one run measures (one GPU; ``--gpus`` above 1 exits with a message):
+
+* ``value``: whole-job throughput of the headline step (C2 at batch 64 by
+  default) in algorithmic GB/s: K timed decode calls back to back, bracketed
+  by ``torch.cuda.synchronize()``, inputs resident in HBM.  Calls rotate over
+  R distinct KV caches whose total exceeds the 256 MB Infinity Cache twice,
+  so the number is an HBM figure ("cold"), not a cache figure.
+* ``roofline``: the decode kernel (one launch per call: split-K phase 1
+  with the log-sum-exp merge fused in) - algorithmic bytes per call divided
+  by its mean launch duration, timed with HIP events on the launch stream
+  around the K back-to-back calls of the timed region; peak 8000 GB/s.
+  ``traffic`` comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+  committed in profiles/traffic.json when present.
+* ``us_per_call``: the reference's latency method (bench/bench_decode.py:
+  86-112 of the reference): each call bracketed by events and followed by a
+  sync, best of 30 after 10 warm-up calls, median of 15 trials, warm inputs,
+  for every batch of the C2 sweep; plus cold GB/s per batch.
+* ``cpu_baseline``: the fp32 CPU oracle (oracle/reference.py, a restatement
+  of the reference's src/reference.py) timed on the host cores on the same
+  headline inputs for a bounded sample (about --cpu-seconds of work), in the
+  same GB/s unit.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+METRIC = "µs/decode call + achieved HBM GB/s (% of peak), GQA 12/2 d128, batch 1–64"
+PEAK_GBS = 8000.0
+MALL_BYTES = 256 * 1024 * 1024
+
+
+def _parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--batch", type=int, default=64, help="C2 batch of the headline step")
+    p.add_argument("--engine", type=int, default=0, help="phase-1 engine: 0 MFMA, 1 VALU/DPP")
+    p.add_argument("--num-splits", type=int, default=0, help="0 = heuristic")
+    p.add_argument("--no-sweep", action="store_true", help="skip the batch sweep")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--trials", type=int, default=15)
+    return p.parse_args()
+
+
+def _rotation(ws_bytes: int) -> int:
+    return max(2, math.ceil(2 * MALL_BYTES / max(ws_bytes, 1)) + 1)
+
+
+def _make_sets(make, n, **kw):
+    return [make(seed=1000 + i, **kw) for i in range(n)]
+
+
+def _call(pad, w, engine, splits):
+    return pad.paged_attention_decode_ex(*w.args(), num_splits=splits or None, engine=engine)
+
+
+def _throughput(pad, sets, engine, splits, steps, warmup):
+    """Seconds per call over `steps` back-to-back calls (events on the launch stream)."""
+    import torch
+
+    for i in range(warmup):
+        _call(pad, sets[i % len(sets)], engine, splits)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        _call(pad, sets[i % len(sets)], engine, splits)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps
+
+
+def _latency_reference_method(pad, w, engine, splits, trials):
+    """bench/bench_decode.py:86-112 of the reference: median of best-of-30 event timings."""
+    import torch
+
+    def once():
+        for _ in range(10):
+            _call(pad, w, engine, splits)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        best = float("inf")
+        for _ in range(30):
+            s.record()
+            _call(pad, w, engine, splits)
+            e.record()
+            torch.cuda.synchronize()
+            best = min(best, s.elapsed_time(e))
+        return best
+
+    return statistics.median([once() for _ in range(trials)]) * 1e3  # µs
+
+
+def _traffic(workload_name):
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        data = json.load(open(path))
+        rec = data.get(workload_name)
+        return None if rec is None else int(rec["bytes_per_call"])
+    except (ValueError, KeyError, TypeError):
+        return None
+
+
+def _cpu_baseline(w, seconds, gpu_out):
+    import torch
+
+    from oracle.reference import paged_attention_decode_reference
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    q = w.q.float().cpu()
+    k = w.k_cache.float().cpu()
+    v = w.v_cache.float().cpu()
+    bt = w.block_table.cpu()
+    sl = w.seq_lens.cpu()
+    times = []
+    out = None
+    t_start = time.perf_counter()
+    while not times or (time.perf_counter() - t_start < seconds and len(times) < 50):
+        t0 = time.perf_counter()
+        out = paged_attention_decode_reference(q, k, v, bt, sl, w.scale)
+        times.append(time.perf_counter() - t0)
+    err = float((gpu_out.float().cpu() - out).abs().max())
+    return statistics.median(times), len(times), torch.get_num_threads(), err
+
+
+def main():
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} (WORLD_SIZE {world}) is not supported. "
+              "The decode path shards by batch or KV head with no exchange; run one process per GPU instead.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import paged_attention_decode_amd as pad
+    from paged_attention_decode_amd import workloads as wl
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    engine = args.engine
+    splits = args.num_splits
+
+    # Headline: C2 at --batch, rotated KV caches (cold).
+    probe = wl.make("C2", batch=args.batch, seed=1000)
+    one_set = probe.k_cache.numel() * 4
+    n_sets = _rotation(one_set)
+    sets = [probe] + _make_sets(wl.make, n_sets - 1, name="C2", batch=args.batch)
+    nbytes = wl.bytes_of(probe)
+    shp = probe.shape
+    plan = pad.plan(shp["batch"], shp["num_q_heads"], shp["num_kv_heads"], shp["head_dim"], shp["page_size"],
+                    shp["max_pages"], splits)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    sec = _throughput(pad, sets, engine, splits, args.steps, args.warmup)
+    wall = time.perf_counter() - t0
+    value = nbytes / sec / 1e9
+    traffic = _traffic(probe.name)
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (fp32 accumulate)",
+        "data": "synthetic (seeded N(0,1) fp16, shuffled block tables)",
+        "config": {
+            "workload": f"C2: batch {args.batch}, seq_len 4096, GQA 12/2, head_dim 128, page 16; "
+                        f"cold (calls rotate over {n_sets} KV caches)",
+            "batch": args.batch,
+            "seq_len": 4096,
+            "num_q_heads": 12,
+            "num_kv_heads": 2,
+            "head_dim": 128,
+            "page_size": 16,
+            "num_splits": plan["num_splits"],
+            "pages_per_split": plan["pages_per_split"],
+            "waves_per_group": plan["waves_per_group"],
+            "engine": "mfma" if engine == 0 else "valu",
+            "algorithmic_bytes_per_call": nbytes,
+        },
+        "pct_of_peak": round(100.0 * value / PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "pad_phase1_kernel",
+            "achieved": round(value, 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(value / PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel_us": round(sec * 1e6, 3),
+            "timed_region_wall_s": round(wall, 4),
+        },
+    }
+    del sets
+
+    if not args.no_sweep:
+        sweep = {}
+        for b in wl.C2_BATCHES:
+            w = wl.make("C2", batch=b, seed=2000 + b)
+            lat = _latency_reference_method(pad, w, engine, splits, args.trials)
+            rs = [w] + _make_sets(wl.make, _rotation(w.k_cache.numel() * 4) - 1, name="C2", batch=b)
+            cold = _throughput(pad, rs, engine, splits, max(20, args.steps // 2), 5)
+            nb = wl.bytes_of(w)
+            sweep[str(b)] = {
+                "us_per_call_warm": round(lat, 2),
+                "us_per_call_cold_throughput": round(cold * 1e6, 2),
+                "gbs_cold": round(nb / cold / 1e9, 1),
+                "pct_of_peak_cold": round(100 * nb / cold / 1e9 / PEAK_GBS, 2),
+            }
+            del rs, w
+        result["c2_sweep"] = sweep
+
+    if not args.no_cpu:
+        gpu_out = _call(pad, probe, engine, splits)
+        torch.cuda.synchronize()
+        med, n, threads, err = _cpu_baseline(probe, args.cpu_seconds, gpu_out)
+        result["cpu_baseline"] = {
+            "value": round(nbytes / med / 1e9, 3),
+            "unit": "GB/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"oracle/reference.py fp32 on the headline C2 batch-{args.batch} inputs, "
+                      f"{n} full call(s), median {med * 1e3:.1f} ms/call, torch threads {threads}",
+            "ms_per_call": round(med * 1e3, 2),
+            "gpu_vs_cpu_max_abs_err": err,
+        }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -29,7 +29,15 @@
  * (cuda/binding.cpp:13-14).  Unlike that launcher, nothing here allocates:
  * the caller passes the output and a workspace sized by
  * pad_decode_workspace_bytes(), and the launch is asynchronous on the
- * caller's stream with no host synchronisation.
+ * caller's stream with no host synchronisation.  Split-K's two phases (the
+ * reference's two kernels) run as one kernel launch.
+ *
+ * Workspace contract.  A workspace holds the fp32 split partials and one
+ * int32 arrival counter per (sequence, kv head).  The counters must be zero
+ * before the first launch that uses the workspace (pad_decode_workspace_init
+ * or any zero-filled allocation); every launch leaves them zero again.  Two
+ * launches that may run at the same time must not share a workspace (give
+ * each stream its own).
  *
  * Every entry point returns a pad_status.  Host-only functions
  * (pad_decode_plan, pad_decode_workspace_bytes, pad_status_string,
@@ -50,7 +58,7 @@ extern "C" {
 /* Largest supported GQA group (query heads per KV head); the reference's
  * bound is the same (cuda/kernel_v4_split_k.cu:44). */
 #define PAD_MAX_GQA 16
-/* Largest split count one call may use (bounded by phase-2 LDS). */
+/* Largest split count one call may use. */
 #define PAD_MAX_SPLITS 1024
 
 typedef enum pad_status {
@@ -91,10 +99,10 @@ typedef struct pad_decode_plan_t {
   int32_t num_splits;       /* splits per (sequence, kv head)              */
   int32_t pages_per_split;
   int32_t waves_per_group;  /* 64-lane waves per phase-1 workgroup         */
-  int32_t single_pass;      /* 1: phase 1 writes `out`, no phase 2         */
+  int32_t single_pass;      /* 1: one split per sequence, no partials      */
   int32_t engine;           /* 0 = MFMA tiles, 1 = VALU/DPP dot products   */
   int32_t reserved;
-  size_t workspace_bytes;   /* fp32 partial (O, m, l) bytes; 0 if single   */
+  size_t workspace_bytes;   /* counters + fp32 partials; 0 if single_pass  */
 } pad_decode_plan_t;
 
 /* Choose the split count and workgroup shape.  num_splits > 0 forces that
@@ -114,6 +122,12 @@ int pad_decode_plan(const pad_decode_dims* dims, int num_splits, int num_cus,
 int pad_decode_workspace_bytes(const pad_decode_dims* dims, int num_splits,
                                int num_cus, size_t* bytes);
 
+/* Zero a workspace (asynchronously, on `stream`) so its arrival counters
+ * start at zero; needed once per workspace.  No counterpart in the
+ * reference, whose launcher allocated fresh partials on every call. */
+int pad_decode_workspace_init(void* workspace, size_t workspace_bytes,
+                              void* stream);
+
 /* Launch the decode on `stream` (a hipStream_t; NULL = the null stream).
  * Asynchronous: returns once the kernels are queued.  `scale` is the
  * softmax scale (the reference defaults it to 1/sqrt(head_dim),
@@ -128,10 +142,10 @@ int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache,
 
 /* Same as pad_decode_launch(), with the engine forced (0 = MFMA tiles,
  * 1 = VALU/DPP dot products) and, when `events` is not NULL, three
- * hipEvent_t handles recorded on `stream` before phase 1, after phase 1
- * and after phase 2 (the third equals the second when single-pass).  For
- * measurement; the outputs are the same as pad_decode_launch()'s.  No
- * counterpart in the reference. */
+ * hipEvent_t handles recorded on `stream`: before the decode kernel, after
+ * it, and at the end of the call (the same point, as the call is one
+ * kernel).  For measurement; the outputs are the same as
+ * pad_decode_launch()'s.  No counterpart in the reference. */
 int pad_decode_launch_ex(const void* q, const void* k_cache,
                          const void* v_cache, const int32_t* block_table,
                          const int32_t* seq_lens, void* out, void* workspace,

@@ -94,6 +94,7 @@ SIGNATURES = {
          ctypes.c_int, ctypes.POINTER(_VP), _VP],
         ctypes.c_int,
     ),
+    "pad_decode_workspace_init": ([_VP, ctypes.c_size_t, _VP], ctypes.c_int),
     "pad_device_num_cus": ([ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "pad_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "pad_decode_abi_version": ([], ctypes.c_int),

@@ -42,6 +42,9 @@ HIP_FLAGS = [
     "-shared",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the online-softmax rescale is VALU work on
+    # them, and AGPR<->VGPR copies around it cost more than they save.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

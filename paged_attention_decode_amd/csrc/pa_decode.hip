@@ -36,10 +36,12 @@
 //    (v_dot2_f32_f16) reduced across the 16 lanes with 4 DPP steps, fp32
 //    online softmax and FMA accumulation of P.V.  Kept for the measured
 //    comparison against engine 0.
-//  * Phase 2 runs one 256-thread workgroup per (b, q head), parallel over
-//    splits and head_dim, with the -inf guard on every split weight.  When a
-//    single split covers every sequence, phase 1 normalises and writes the
-//    fp16 output itself and phase 2 is not launched.
+//  * Phase 2 is fused into the same launch: every workgroup of a split
+//    sequence publishes its fp32 partial with device-scope stores and counts
+//    itself in with an atomic; the last one to arrive folds all partials of
+//    its (sequence, kv head) into the fp16 output and resets the counter.  A
+//    sequence held by one split is normalised directly.  One kernel launch
+//    per call.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -58,8 +60,10 @@ constexpr float kNegInf = -__builtin_inff();
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBlockTokens = 16;  // tokens per wave iteration (one MFMA tile)
 constexpr int kMaxWaves = 4;
-constexpr int kPhase2Threads = 256;
 constexpr int kMergeLdsBudget = 48 * 1024;  // bytes of LDS for the wave merge
+// Headroom (base-2 units) a score may exceed the running reference max before
+// the accumulators are rescaled; fp16 weights stay <= 2^8.
+constexpr float kRescaleSlack = 8.0f;
 
 struct Phase1Args {
   const _Float16* q;
@@ -70,6 +74,7 @@ struct Phase1Args {
   _Float16* out;
   float* o_part;   // [B, Hkv, S, gqa, D]
   float2* ml_part; // [B, Hkv, S, gqa]  (m in base-2 units, l)
+  int* counters;   // [B, Hkv] arrival counts, zero between launches
   int64_t sqb, sqh;
   int64_t skp, sks, skh;
   int64_t svp, svs, svh;
@@ -78,17 +83,7 @@ struct Phase1Args {
   int64_t sob, soh;
   int64_t num_pages;
   int gqa, ps, pps, num_splits, hkv, max_pages;
-  int single;  // 1: this launch covers whole sequences and writes `out`
   float scale_log2;
-};
-
-struct Phase2Args {
-  const float* o_part;
-  const float2* ml_part;
-  const int32_t* sl;
-  _Float16* out;
-  int64_t ssl, sob, soh;
-  int gqa, ps, pps, num_splits, hkv, max_pages;
 };
 
 __device__ __forceinline__ float exp2_fast(float x) {
@@ -149,6 +144,58 @@ __device__ __forceinline__ HVec<NDW> load_hvec(const _Float16* p) {
   return r;
 }
 
+// Same as load_hvec, with the non-temporal hint: K/V are streamed once per
+// call, so they should not displace the reused lines (q, block_table,
+// partials) in the caches.
+template <int NDW>
+__device__ __forceinline__ HVec<NDW> load_hvec_stream(const _Float16* p) {
+  typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+  typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+  HVec<NDW> r;
+  if constexpr (NDW % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < NDW / 4; ++i) {
+      const u4_t x = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p) + i);
+      r.w[4 * i + 0] = x[0]; r.w[4 * i + 1] = x[1]; r.w[4 * i + 2] = x[2]; r.w[4 * i + 3] = x[3];
+    }
+  } else if constexpr (NDW % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < NDW / 2; ++i) {
+      const u2_t x = __builtin_nontemporal_load(reinterpret_cast<const u2_t*>(p) + i);
+      r.w[2 * i + 0] = x[0]; r.w[2 * i + 1] = x[1];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NDW; ++i) r.w[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p) + i);
+  }
+  return r;
+}
+
+// Raw buffer resource over [base, base + bytes) (gfx9 raw-buffer word 3:
+// 32-bit data format, no swizzle); out-of-range accesses are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Device-scope (SC1) accesses: coherent across all CUs and XCDs without
+// cache maintenance instructions.
+constexpr int kCachePolicyDevice = 16;  // SC1
+typedef int32_t i2_t __attribute__((ext_vector_type(2)));
+typedef int32_t i4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void store_device(__amdgpu_buffer_rsrc_t r, uint32_t off, f4_t v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i4_t, v), r, off, 0, kCachePolicyDevice);
+}
+__device__ __forceinline__ void store_device(__amdgpu_buffer_rsrc_t r, uint32_t off, float2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(i2_t, v), r, off, 0, kCachePolicyDevice);
+}
+__device__ __forceinline__ f4_t load_device_f4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCachePolicyDevice));
+}
+__device__ __forceinline__ float2 load_device_f2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCachePolicyDevice));
+}
+
 __device__ __forceinline__ int clamp_page(int phys, int64_t num_pages) {
   // Keeps every access inside the cache for an invalid block_table entry
   // (the reference documents valid ids as a precondition and does not
@@ -162,7 +209,15 @@ __device__ __forceinline__ int clamp_page(int phys, int64_t num_pages) {
 // for both engines:  sm_ml[w*16 + row] = (m, l),  sm_o[(w*gqa + row)*D + d].
 // ---------------------------------------------------------------------------
 
-// Engine 0: MFMA 16x16x16 f16 tiles.
+// One 16-token block of K and V in registers, in the MFMA operand layouts.
+template <int D>
+struct KVTile {
+  h8_t k[D / 32];       // K[token r16][kp*32 + g*8 + 0..7]
+  HVec<D / 32> v[4];    // V[token 4g+i][r16*(D/16) + 0..D/16-1]
+};
+
+// Engine 0: MFMA 16x16x16 f16 tiles, two blocks in flight per wave (the
+// loads of block j+nw are issued before block j is computed).
 template <int D, bool UNIFORM>
 __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int b, int kvh, int t_begin,
                                                int t_end, int nblk, int wave, int nw, int lane,
@@ -191,63 +246,68 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int b, int k
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = (f4_t)0.f;
 
-  const int64_t koff_h = (int64_t)kvh * a.skh;
-  const int64_t voff_h = (int64_t)kvh * a.svh;
+  const char* k_head = reinterpret_cast<const char*>(a.k + (int64_t)kvh * a.skh);
+  const char* v_head = reinterpret_cast<const char*>(a.v + (int64_t)kvh * a.svh);
   const int32_t* bt_row = a.bt + (int64_t)b * a.sbb;
-
-  for (int j = wave; j < nblk; j += nw) {
-    const int t0 = t_begin + j * kBlockTokens;
-    const bool full = t0 + kBlockTokens <= t_end;
-    const _Float16* krow;
-    const _Float16* vrow[4];
-    if constexpr (UNIFORM) {
-      // page_size % 16 == 0 and splits start on page boundaries: the whole
-      // block lives in one page, so the page id is wave-uniform.
-      const int page = t0 / a.ps;
-      const int phys = clamp_page(__builtin_amdgcn_readfirstlane(bt_row[(int64_t)page * a.sbp]), a.num_pages);
-      const int slot0 = t0 - page * a.ps;
-      const _Float16* kbase = a.k + (int64_t)phys * a.skp + koff_h + (int64_t)slot0 * a.sks;
-      const _Float16* vbase = a.v + (int64_t)phys * a.svp + voff_h + (int64_t)slot0 * a.svs;
-      krow = kbase + (int64_t)r16 * a.sks;
+  // Lane byte offsets inside a 16-token slab of one page (loop invariant).
+  const uint32_t koff = (uint32_t)(((int64_t)r16 * a.sks + g * 8) * 2);
+  uint32_t voff[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vrow[i] = vbase + (int64_t)(4 * g + i) * a.svs;
+  for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((int64_t)(4 * g + i) * a.svs + r16 * DT) * 2);
+  const int blocks_per_page = a.ps / kBlockTokens;  // UNIFORM only
+  const int p_first = t_begin / a.ps;
+
+  auto load = [&](KVTile<D>& t, int jb) {
+    if constexpr (UNIFORM) {
+      // page_size % 16 == 0 and splits start on page boundaries: the block
+      // lives in one page, so its page id and base address are wave-uniform.
+      const int jp = jb / blocks_per_page;
+      const int page = p_first + jp;
+      const int slot0 = (jb - jp * blocks_per_page) * kBlockTokens;
+      const int phys = clamp_page(__builtin_amdgcn_readfirstlane(bt_row[(int64_t)page * a.sbp]), a.num_pages);
+      const char* kb = k_head + ((int64_t)phys * a.skp + (int64_t)slot0 * a.sks) * 2;
+      const char* vb = v_head + ((int64_t)phys * a.svp + (int64_t)slot0 * a.svs) * 2;
+#pragma unroll
+      for (int kp = 0; kp < DK; ++kp) t.k[kp] = __builtin_nontemporal_load(reinterpret_cast<const h8_t*>(kb + koff + kp * 64));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(vb + voff[i]));
     } else {
       // Any page size: each token looks up its own page; tokens past the
-      // end are clamped to the last valid token (and masked below).
+      // end are clamped to the last valid token (and masked in compute).
+      const int t0 = t_begin + jb * kBlockTokens;
       {
         const int tk = min(t0 + r16, t_end - 1);
         const int page = tk / a.ps;
         const int phys = clamp_page(bt_row[(int64_t)page * a.sbp], a.num_pages);
-        krow = a.k + (int64_t)phys * a.skp + koff_h + (int64_t)(tk - page * a.ps) * a.sks;
+        const char* kr = k_head + ((int64_t)phys * a.skp + (int64_t)(tk - page * a.ps) * a.sks + g * 8) * 2;
+#pragma unroll
+        for (int kp = 0; kp < DK; ++kp) t.k[kp] = __builtin_nontemporal_load(reinterpret_cast<const h8_t*>(kr + kp * 64));
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tv = min(t0 + 4 * g + i, t_end - 1);
         const int page = tv / a.ps;
         const int phys = clamp_page(bt_row[(int64_t)page * a.sbp], a.num_pages);
-        vrow[i] = a.v + (int64_t)phys * a.svp + voff_h + (int64_t)(tv - page * a.ps) * a.svs;
+        const char* vr = v_head + ((int64_t)phys * a.svp + (int64_t)(tv - page * a.ps) * a.svs + r16 * DT) * 2;
+        t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(vr));
       }
     }
+  };
 
-    h8_t kk[DK];
-#pragma unroll
-    for (int kp = 0; kp < DK; ++kp) kk[kp] = *reinterpret_cast<const h8_t*>(krow + kp * 32 + g * 8);
-    HVec<NDW> vv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) vv[i] = load_hvec<NDW>(vrow[i] + r16 * DT);
-
+  auto compute = [&](KVTile<D>& t, int jb) {
+    const int t0 = t_begin + jb * kBlockTokens;
+    const bool full = t0 + kBlockTokens <= t_end;
     // S^T[token 4g+i][row r16] over head_dim.
     f4_t sacc = (f4_t)0.f;
 #pragma unroll
     for (int kp = 0; kp < DK; ++kp) {
-      const h4_t k_lo = __builtin_shufflevector(kk[kp], kk[kp], 0, 1, 2, 3);
-      const h4_t k_hi = __builtin_shufflevector(kk[kp], kk[kp], 4, 5, 6, 7);
+      const h4_t k_lo = __builtin_shufflevector(t.k[kp], t.k[kp], 0, 1, 2, 3);
+      const h4_t k_hi = __builtin_shufflevector(t.k[kp], t.k[kp], 4, 5, 6, 7);
       const h4_t q_lo = __builtin_shufflevector(qv[kp], qv[kp], 0, 1, 2, 3);
       const h4_t q_hi = __builtin_shufflevector(qv[kp], qv[kp], 4, 5, 6, 7);
       sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k_lo, q_lo, sacc, 0, 0, 0);
       sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k_hi, q_hi, sacc, 0, 0, 0);
     }
-
     float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = sacc[i] * a.scale_log2;
@@ -256,32 +316,64 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int b, int k
       for (int i = 0; i < 4; ++i) {
         const bool valid = t0 + 4 * g + i < t_end;
         x[i] = valid ? x[i] : kNegInf;
-        if (!valid) vv[i].zero();  // stale cache slots may hold NaN/Inf
+        if (!valid) t.v[i].zero();  // stale cache slots may hold NaN/Inf
       }
     }
     float bm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
     bm = fmaxf(bm, shfl_xor_f(bm, 16));
     bm = fmaxf(bm, shfl_xor_f(bm, 32));
-    // Every block holds at least one valid token, so m_new is finite.
-    const float m_new = fmaxf(m_run, bm);
-    const float alpha = exp2_fast(m_run - m_new);
+    // Lazy rescaling: the reference m_run only moves when a score exceeds it
+    // by more than kRescaleSlack (base-2 units), so weights stay <= 2^slack
+    // and the O/l rescale is skipped (wave-uniformly) on most blocks.  Any
+    // reference value gives the same O/l; partials carry it as their m.
+    // Every block holds at least one valid token, so bm is finite.
+    if (__builtin_amdgcn_ballot_w64(bm > m_run + kRescaleSlack) != 0) {
+      const float m_new = fmaxf(m_run, bm);
+      const float alpha = exp2_fast(m_run - m_new);  // 0 on the first block
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+      m_run = m_new;
+    }
     h4_t ph;
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const _Float16 p = (_Float16)exp2_fast(x[i] - m_new);
+      const _Float16 p = (_Float16)exp2_fast(x[i] - m_run);
       ph[i] = p;
       psum += (float)p;  // l accumulates the same rounded weights P.V uses
     }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-
+    l_run += psum;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       h4_t av;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = vv[i].h(dt);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, o[dt] * alpha, 0, 0, 0);
+      for (int i = 0; i < 4; ++i) av[i] = t.v[i].h(dt);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, o[dt], 0, 0, 0);
+    }
+  };
+
+  // This wave's blocks are wave, wave+nw, ...  The steady-state loop issues
+  // the next block's loads unconditionally before computing the current one
+  // (no control-flow join on the in-flight registers); the last one or two
+  // blocks are peeled.
+  const int n_mine = wave < nblk ? (nblk - wave + nw - 1) / nw : 0;
+  KVTile<D> ta, tb;
+  if (n_mine > 0) {
+    int it = 0;
+    load(ta, wave);
+    for (; it + 2 < n_mine; it += 2) {
+      load(tb, wave + (it + 1) * nw);
+      compute(ta, wave + it * nw);
+      load(ta, wave + (it + 2) * nw);
+      compute(tb, wave + (it + 1) * nw);
+    }
+    if (it + 1 < n_mine) {
+      load(tb, wave + (it + 1) * nw);
+      compute(ta, wave + it * nw);
+      compute(tb, wave + (it + 1) * nw);
+    } else {
+      compute(ta, wave + it * nw);
     }
   }
 
@@ -433,9 +525,17 @@ __device__ __forceinline__ void wave_loop_valu(const Phase1Args& a, int b, int k
   }
 }
 
+// Minimum waves per SIMD each phase-1 instantiation is compiled for (it
+// caps the registers per lane at 512 / waves).  The split heuristic sizes the
+// grid to one round of resident waves using the same numbers.
+constexpr int phase1_waves_per_simd(int d, int engine) {
+  return engine == 0 ? (d <= 128 ? 3 : 1) : 1;
+}
+
 // Phase 1: one workgroup per (split, kv head, sequence).
 template <int D, bool UNIFORM, int ENGINE, int GQA_T>
-__global__ __launch_bounds__(256) void pad_phase1_kernel(const Phase1Args a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE))))
+void pad_phase1_kernel(const Phase1Args a) {
   extern __shared__ float4 smem_f4[];
   float2* sm_ml = reinterpret_cast<float2*>(smem_f4);  // [nw][16]
   const int nw = blockDim.x >> 6;
@@ -445,15 +545,27 @@ __global__ __launch_bounds__(256) void pad_phase1_kernel(const Phase1Args a) {
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
   const int L = max(a.sl[(int64_t)b * a.ssl], 0);
   const int npages = min((L + a.ps - 1) / a.ps, a.max_pages);
+  const int nsplit = (npages + a.pps - 1) / a.pps;  // non-empty splits of this sequence
+  const int gqa = a.gqa;
+  const int total4 = gqa * (D / 4);
+  _Float16* out_bh = a.out + (int64_t)b * a.sob + (int64_t)(kvh * gqa) * a.soh;
+  if (s >= nsplit) {  // empty split
+    if (s == 0) {     // seq_len == 0: the output rows are zeros
+      for (int e = threadIdx.x; e < total4; e += blockDim.x) {
+        const int row = e / (D / 4);
+        *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + (e - row * (D / 4)) * 4) = (h4_t)0;
+      }
+    }
+    return;
+  }
   const int p0 = s * a.pps;
-  if (!a.single && p0 >= npages) return;  // empty split: phase 2 never reads it
   const int t_begin = p0 * a.ps;
   const int t_end = min(min(p0 + a.pps, npages) * a.ps, L);
-  const int nblk = t_end > t_begin ? (t_end - t_begin + kBlockTokens - 1) / kBlockTokens : 0;
+  const int nblk = (t_end - t_begin + kBlockTokens - 1) / kBlockTokens;
 
   if constexpr (ENGINE == 0) {
     wave_loop_mfma<D, UNIFORM>(a, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o);
@@ -462,10 +574,16 @@ __global__ __launch_bounds__(256) void pad_phase1_kernel(const Phase1Args a) {
   }
   __syncthreads();
 
-  // Merge the waves' states: threads over (row, 4 consecutive d).
-  const int gqa = a.gqa;
-  const int total4 = gqa * (D / 4);
-  const int64_t part_row0 = (((int64_t)b * a.hkv + kvh) * a.num_splits + s) * gqa;
+  // Merge the waves' states: threads over (row, 4 consecutive d).  With a
+  // single split the result is final; otherwise it is this split's partial.
+  // Partials are stored and later loaded with device-scope (SC1) buffer
+  // accesses, which are coherent across the XCDs' L2 caches on their own, so
+  // publishing a partial needs no cache writeback.  Each (sequence, kv head)
+  // owns a contiguous partial region, addressed with 32-bit byte offsets.
+  const int64_t seq_row0 = ((int64_t)b * a.hkv + kvh) * a.num_splits * gqa;
+  const uint32_t region_rows = (uint32_t)(a.num_splits * gqa);
+  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o_part + seq_row0 * D, region_rows * D * 4u);
+  const __amdgpu_buffer_rsrc_t ml_rsrc = make_rsrc(a.ml_part + seq_row0, region_rows * 8u);
   for (int e = threadIdx.x; e < total4; e += blockDim.x) {
     const int row = e / (D / 4);
     const int col = (e - row * (D / 4)) * 4;
@@ -473,110 +591,66 @@ __global__ __launch_bounds__(256) void pad_phase1_kernel(const Phase1Args a) {
     for (int w = 0; w < nw; ++w) M = fmaxf(M, sm_ml[w * 16 + row].x);
     f4_t acc = (f4_t)0.f;
     float Ls = 0.f;
-    if (M != kNegInf) {
-      for (int w = 0; w < nw; ++w) {
-        const float2 ml = sm_ml[w * 16 + row];
-        const float c = (ml.x == kNegInf) ? 0.f : exp2_fast(ml.x - M);
-        Ls += c * ml.y;
-        acc += c * *reinterpret_cast<const f4_t*>(sm_o + (w * gqa + row) * D + col);
-      }
+    for (int w = 0; w < nw; ++w) {
+      const float2 ml = sm_ml[w * 16 + row];
+      const float c = (ml.x == kNegInf) ? 0.f : exp2_fast(ml.x - M);
+      Ls += c * ml.y;
+      acc += c * *reinterpret_cast<const f4_t*>(sm_o + (w * gqa + row) * D + col);
     }
-    if (a.single) {
-      const float inv = Ls > 0.f ? 1.f / Ls : 0.f;  // seq_len == 0 -> zeros
+    if (nsplit == 1) {
+      const float inv = 1.f / Ls;  // Ls >= 1: the max token contributes 2^0
       h4_t hv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
-      *reinterpret_cast<h4_t*>(a.out + (int64_t)b * a.sob + (int64_t)(kvh * gqa + row) * a.soh + col) = hv;
+      *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + col) = hv;
     } else {
-      *reinterpret_cast<f4_t*>(a.o_part + (part_row0 + row) * D + col) = acc;
-      if (col == 0) a.ml_part[part_row0 + row] = make_float2(M, Ls);
+      const uint32_t r = (uint32_t)(s * gqa + row);
+      store_device(o_rsrc, (r * D + col) * 4u, acc);
+      if (col == 0) store_device(ml_rsrc, r * 8u, make_float2(M, Ls));
     }
   }
-}
+  if (nsplit == 1) return;
 
-// Phase 2: one workgroup per (q head, sequence): LSE merge over splits.
-template <int D>
-__global__ __launch_bounds__(kPhase2Threads) void pad_phase2_kernel(const Phase2Args a) {
-  __shared__ float s_w[PAD_MAX_SPLITS];
-  __shared__ f4_t s_acc[kPhase2Threads];
-  __shared__ float s_red[kPhase2Threads / 64];
-  __shared__ float s_bcast;
-
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const int tid = threadIdx.x;
-  const int kvh = h / a.gqa;
-  const int row = h - kvh * a.gqa;
-  _Float16* orow = a.out + (int64_t)b * a.sob + (int64_t)h * a.soh;
-
-  const int L = max(a.sl[(int64_t)b * a.ssl], 0);
-  const int npages = min((L + a.ps - 1) / a.ps, a.max_pages);
-  const int nsplit = min((npages + a.pps - 1) / a.pps, a.num_splits);
-  if (nsplit == 0) {  // seq_len == 0 -> zeros
-    for (int d = tid; d < D; d += kPhase2Threads) orow[d] = (_Float16)0.f;
-    return;
-  }
-  const int64_t base = (((int64_t)b * a.hkv + kvh) * a.num_splits) * a.gqa + row;
-  const int64_t sstride = a.gqa;
-
-  // Pass 1: global max of the split maxima.
-  float mx = kNegInf;
-  for (int s = tid; s < nsplit; s += kPhase2Threads) mx = fmaxf(mx, a.ml_part[base + s * sstride].x);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if ((tid & 63) == 0) s_red[tid >> 6] = mx;
+  // Split-K merge, fused: the last workgroup of this (sequence, kv head) to
+  // arrive folds every split's partial into the output.  A workgroup counts
+  // itself in only after its partial stores have completed at device scope
+  // (vmcnt(0) covers stores on this architecture); the last one to arrive
+  // reads the partials with device-scope loads and resets the counter to
+  // zero for the next launch.
+  __shared__ int s_last;
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (tid == 0) {
-    float v = s_red[0];
-    for (int w = 1; w < kPhase2Threads / 64; ++w) v = fmaxf(v, s_red[w]);
-    s_bcast = v;
+  if (threadIdx.x == 0) {
+    const int prev = atomicAdd(a.counters + (int64_t)b * a.hkv + kvh, 1);
+    s_last = (prev == nsplit - 1);
   }
   __syncthreads();
-  const float M = s_bcast;
-
-  // Pass 2: split weights and the total l.
-  float ls = 0.f;
-  for (int s = tid; s < nsplit; s += kPhase2Threads) {
-    const float2 ml = a.ml_part[base + s * sstride];
-    const float w = (ml.x == kNegInf) ? 0.f : exp2_fast(ml.x - M);
-    s_w[s] = w;
-    ls += w * ml.y;
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) ls += __shfl_xor(ls, off, 64);
-  __syncthreads();  // s_red reuse + s_w visible
-  if ((tid & 63) == 0) s_red[tid >> 6] = ls;
-  __syncthreads();
-  if (tid == 0) {
-    float v = 0.f;
-    for (int w = 0; w < kPhase2Threads / 64; ++w) v += s_red[w];
-    s_bcast = v;
-  }
-  __syncthreads();
-  const float Ltot = s_bcast;
-
-  // Pass 3: weighted sum of the partial outputs, float4 per thread.
-  constexpr int TPR = D / 4;                   // threads per split row
-  constexpr int SG = kPhase2Threads / TPR;     // split groups
-  const int sg = tid / TPR;
-  const int c4 = tid - sg * TPR;
-  f4_t acc = (f4_t)0.f;
-  if (sg < SG) {
-    for (int s = sg; s < nsplit; s += SG) {
-      const f4_t o = *reinterpret_cast<const f4_t*>(a.o_part + (base + s * sstride) * D + c4 * 4);
-      acc += s_w[s] * o;
+  if (!s_last) return;
+  for (int e = threadIdx.x; e < total4; e += blockDim.x) {
+    const int row = e / (D / 4);
+    const int col = (e - row * (D / 4)) * 4;
+    float m = kNegInf, l = 0.f;
+    f4_t acc = (f4_t)0.f;
+#pragma unroll 8
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const uint32_t r = (uint32_t)(sp * gqa + row);
+      const float2 ml = load_device_f2(ml_rsrc, r * 8u);
+      const f4_t o = load_device_f4(o_rsrc, (r * D + col) * 4u);
+      // Every published split is non-empty, so ml.x is finite.
+      const float m_new = fmaxf(m, ml.x);
+      const float alpha = exp2_fast(m - m_new);  // 0 while m is -inf
+      const float beta = exp2_fast(ml.x - m_new);
+      l = l * alpha + ml.y * beta;
+      acc = acc * alpha + o * beta;
+      m = m_new;
     }
-  }
-  s_acc[tid] = acc;
-  __syncthreads();
-  if (sg == 0) {
-    for (int g2 = 1; g2 < SG; ++g2) acc += s_acc[g2 * TPR + c4];
-    const float inv = Ltot > 0.f ? 1.f / Ltot : 0.f;
+    const float inv = 1.f / l;
     h4_t hv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
-    *reinterpret_cast<h4_t*>(orow + c4 * 4) = hv;
+    *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + col) = hv;
   }
+  if (threadIdx.x == 0) atomicExch(a.counters + (int64_t)b * a.hkv + kvh, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -611,6 +685,28 @@ static int validate_dims(const pad_decode_dims* d) {
   return PAD_OK;
 }
 
+// Workspace layout (from the first 256-byte boundary of the buffer):
+//   counters int32 [B*Hkv]            arrival counts; zero between launches
+//   o_part   fp32  [B, Hkv, S, gqa, D] unnormalised split outputs
+//   ml_part  fp32x2 [B, Hkv, S, gqa]   (m in base-2 units, l)
+// Returns the bytes needed (including 256 bytes of alignment slack) and,
+// when `ws` is given, the region pointers.
+static size_t workspace_layout(const pad_decode_dims* d, int S, void* ws, int** counters, float** o_part,
+                               float2** ml_part) {
+  const int gqa = d->num_q_heads / d->num_kv_heads;
+  const size_t units = (size_t)d->batch * d->num_kv_heads;
+  const size_t counter_bytes = (units * sizeof(int) + 255u) & ~(size_t)255u;
+  const size_t rows = units * (size_t)S * gqa;
+  const size_t o_bytes = rows * (size_t)d->head_dim * sizeof(float);
+  if (ws) {
+    const uintptr_t base = ((uintptr_t)ws + 255u) & ~(uintptr_t)255u;
+    *counters = reinterpret_cast<int*>(base);
+    *o_part = reinterpret_cast<float*>(base + counter_bytes);
+    *ml_part = reinterpret_cast<float2*>(base + counter_bytes + o_bytes);
+  }
+  return 256 + counter_bytes + o_bytes + rows * sizeof(float2);
+}
+
 static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int engine,
                      pad_decode_plan_t* p) {
   const int st = validate_dims(d);
@@ -629,14 +725,15 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     S = num_splits;
     pps = ceil_div(max_pages, S);
   } else {
-    // Heuristic: enough workgroups to cover every CU a few times, but never
-    // fewer than kMinBlocks 16-token blocks per split, so the fp32 partial
-    // traffic (gqa*(D+2)*4 bytes per split) stays a small fraction of the
-    // split's K/V bytes (page_size*Hkv-share*D*4 per page).
-    const int kTargetGroups = 4 * num_cus;
-    const int kMinBlocks = 4;
+    // Heuristic: one round of resident waves.  The grid (batch x kv heads x
+    // splits workgroups of kMaxWaves waves) is sized to the waves the CUs
+    // hold at once for this kernel, so no workgroup waits for a second
+    // round, and a split never has fewer than kMinBlocks 16-token blocks
+    // (one per wave), which also bounds the fp32 partial traffic.
+    const int kMinBlocks = kMaxWaves;
+    const int64_t resident_waves = (int64_t)num_cus * 4 * phase1_waves_per_simd(d->head_dim, 0);
     const int64_t blocks_per_seq = ((int64_t)max_pages * d->page_size + kBlockTokens - 1) / kBlockTokens;
-    int64_t s_want = (kTargetGroups + units - 1) / units;
+    int64_t s_want = resident_waves / (units * kMaxWaves);
     int64_t s_cap = blocks_per_seq / kMinBlocks;
     if (s_cap < 1) s_cap = 1;
     if (s_want > s_cap) s_want = s_cap;
@@ -657,8 +754,7 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   p->single_pass = (S == 1) ? 1 : 0;
   p->engine = engine;
   p->reserved = 0;
-  p->workspace_bytes =
-      p->single_pass ? 0 : (size_t)d->batch * d->num_kv_heads * S * gqa * (size_t)(d->head_dim + 2) * 4 + 256;
+  p->workspace_bytes = p->single_pass ? 0 : workspace_layout(d, S, nullptr, nullptr, nullptr, nullptr);
   return PAD_OK;
 }
 
@@ -707,12 +803,6 @@ static hipError_t dispatch_phase1(const Phase1Args& a, dim3 grid, int nw, size_t
   return dispatch_engine<D, false>(a, grid, nw, lds, engine, st);
 }
 
-template <int D>
-static hipError_t launch_p2(const Phase2Args& a, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((pad_phase2_kernel<D>), grid, dim3(kPhase2Threads), 0, st, a);
-  return hipGetLastError();
-}
-
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 static int launch_impl(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
@@ -739,14 +829,10 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
 
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   const int S = plan.num_splits;
+  int* counters = nullptr;
   float* o_part = nullptr;
   float2* ml_part = nullptr;
-  if (!plan.single_pass) {
-    uintptr_t base = ((uintptr_t)ws + 255u) & ~(uintptr_t)255u;
-    o_part = reinterpret_cast<float*>(base);
-    const size_t o_elems = (size_t)d->batch * d->num_kv_heads * S * gqa * d->head_dim;
-    ml_part = reinterpret_cast<float2*>(o_part + o_elems);
-  }
+  if (!plan.single_pass) workspace_layout(d, S, ws, &counters, &o_part, &ml_part);
 
   Phase1Args a;
   a.q = static_cast<const _Float16*>(q);
@@ -757,6 +843,7 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.out = static_cast<_Float16*>(out);
   a.o_part = o_part;
   a.ml_part = ml_part;
+  a.counters = counters;
   a.sqb = d->q_stride[0];
   a.sqh = d->q_stride[1];
   a.skp = d->k_stride[0];
@@ -777,7 +864,6 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.num_splits = S;
   a.hkv = d->num_kv_heads;
   a.max_pages = d->max_pages;
-  a.single = plan.single_pass;
   a.scale_log2 = scale * kLog2e;
 
   const int nw = plan.waves_per_group;
@@ -797,32 +883,6 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   if (e != hipSuccess) return PAD_ERR_LAUNCH;
   if (events && events[1] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[1]), hs) != hipSuccess)
     return PAD_ERR_LAUNCH;
-
-  if (!plan.single_pass) {
-    Phase2Args p2;
-    p2.o_part = o_part;
-    p2.ml_part = ml_part;
-    p2.sl = sl;
-    p2.out = a.out;
-    p2.ssl = a.ssl;
-    p2.sob = a.sob;
-    p2.soh = a.soh;
-    p2.gqa = gqa;
-    p2.ps = a.ps;
-    p2.pps = a.pps;
-    p2.num_splits = S;
-    p2.hkv = a.hkv;
-    p2.max_pages = a.max_pages;
-    const dim3 grid2(d->num_q_heads, d->batch);
-    switch (d->head_dim) {
-      case 32: e = launch_p2<32>(p2, grid2, hs); break;
-      case 64: e = launch_p2<64>(p2, grid2, hs); break;
-      case 96: e = launch_p2<96>(p2, grid2, hs); break;
-      case 128: e = launch_p2<128>(p2, grid2, hs); break;
-      default: e = launch_p2<256>(p2, grid2, hs); break;
-    }
-    if (e != hipSuccess) return PAD_ERR_LAUNCH;
-  }
   if (events && events[2] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[2]), hs) != hipSuccess)
     return PAD_ERR_LAUNCH;
   return PAD_OK;
@@ -859,6 +919,14 @@ int pad_decode_launch_ex(const void* q, const void* k_cache, const void* v_cache
                          void* const* events, void* stream) {
   return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, out, workspace, workspace_bytes, dims,
                           scale, num_splits, engine, events, stream);
+}
+
+int pad_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace) return PAD_ERR_NULL_POINTER;
+  if (workspace_bytes == 0) return PAD_OK;
+  return hipMemsetAsync(workspace, 0, workspace_bytes, reinterpret_cast<hipStream_t>(stream)) == hipSuccess
+             ? PAD_OK
+             : PAD_ERR_LAUNCH;
 }
 
 int pad_device_num_cus(int* num_cus) {

@@ -4,8 +4,9 @@
 // `forward_v4` entry called paged_attn_decode_cuda_v4_launch
 // (cuda/kernel_v4_split_k.cu:205-268).  This file holds no kernels: it reads
 // shapes, strides and data pointers from the tensors, allocates the output
-// and the fp32 split workspace from PyTorch's caching allocator, and calls
-// pad_decode_launch_ex() on PyTorch's current HIP stream of q's device.
+// from PyTorch's caching allocator, and calls
+// pad_decode_launch_ex() on PyTorch's current HIP stream of q's device, with
+// a persistent workspace per (device, stream).
 // Argument errors surface as RuntimeError (the reference used TORCH_CHECK,
 // cuda/kernel_v4_split_k.cu:216-223).  No host synchronisation.
 
@@ -13,6 +14,9 @@
 
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <map>
+#include <utility>
 
 #include "pa_decode.h"
 
@@ -27,6 +31,21 @@ int cached_cus(int device) {
     cus[device] = n;
   }
   return cus[device];
+}
+
+// One persistent, zero-initialised workspace per (device, stream): the
+// kernels' arrival counters must start at zero and are left at zero by every
+// launch, and launches on one stream are ordered, so reusing the buffer on
+// its stream is safe.  It grows (a fresh zeroed buffer, allocated and filled
+// on the same stream) when a call needs more.
+void* stream_workspace(const torch::Tensor& like, hipStream_t stream, size_t bytes) {
+  static std::map<std::pair<int, uintptr_t>, torch::Tensor> cache;
+  torch::Tensor& ws = cache[{like.get_device(), reinterpret_cast<uintptr_t>(stream)}];
+  if (!ws.defined() || static_cast<size_t>(ws.numel()) < bytes) {
+    const int64_t grown = static_cast<int64_t>(((bytes + (1u << 20) - 1) >> 20) << 20);
+    ws = torch::zeros({grown}, like.options().dtype(at::kByte));
+  }
+  return ws.data_ptr();
 }
 
 void fill_dims(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
@@ -50,9 +69,9 @@ void fill_dims(const torch::Tensor& q, const torch::Tensor& k, const torch::Tens
   for (int i = 0; i < 3; ++i) d->out_stride[i] = out.stride(i);
 }
 
-torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
-                      torch::Tensor block_table, torch::Tensor seq_lens, double scale,
-                      int64_t num_splits, int64_t engine) {
+torch::Tensor forward_impl(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                           torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                           int64_t num_splits, int64_t engine, void* const* events) {
   TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && block_table.is_cuda() &&
                   seq_lens.is_cuda(),
               "pa_decode: all tensors must be on the GPU");
@@ -81,19 +100,31 @@ torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_ca
   size_t ws_bytes = 0;
   int st = pad_decode_workspace_bytes(&d, static_cast<int>(num_splits), cus, &ws_bytes);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  torch::Tensor ws;
-  void* ws_ptr = nullptr;
-  if (ws_bytes > 0) {
-    ws = torch::empty({static_cast<int64_t>(ws_bytes)}, q.options().dtype(at::kByte));
-    ws_ptr = ws.data_ptr();
-  }
   hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  void* ws_ptr = nullptr;
+  if (ws_bytes > 0) ws_ptr = stream_workspace(q, stream, ws_bytes);
   st = pad_decode_launch_ex(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                             block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
                             ws_ptr, ws_bytes, &d, static_cast<float>(scale), static_cast<int>(num_splits),
-                            static_cast<int>(engine), nullptr, stream);
+                            static_cast<int>(engine), events, stream);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   return out;
+}
+
+torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                      torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                      int64_t num_splits, int64_t engine) {
+  return forward_impl(q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, engine, nullptr);
+}
+
+// forward() that also records three hipEvent_t handles (raw handles as
+// integers, e.g. torch.cuda.Event.cuda_event): before the kernel, after it,
+// and at the end of the call.
+torch::Tensor forward_events(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                             torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                             int64_t num_splits, int64_t engine, int64_t ev0, int64_t ev1, int64_t ev2) {
+  void* evs[3] = {reinterpret_cast<void*>(ev0), reinterpret_cast<void*>(ev1), reinterpret_cast<void*>(ev2)};
+  return forward_impl(q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, engine, evs);
 }
 
 // Same argument list as the reference's forward_v4 binding
@@ -141,6 +172,8 @@ py::dict plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward", &forward, "Paged-attention decode (q, k_cache, v_cache, block_table, seq_lens, scale, "
                              "num_splits, engine) -> out");
+  m.def("forward_events", &forward_events,
+        "forward() recording three hipEvent_t handles: before phase 1, after phase 1, after phase 2");
   m.def("forward_v4", &forward_v4, "Paged-attention decode with the reference forward_v4 argument list");
   m.def("plan", &plan, "Split plan for the given shapes (host only)");
   m.def("abi_version", &pad_decode_abi_version, "C ABI version of the linked libpa_decode.so");

@@ -9,7 +9,9 @@ large batches (profiles/notes.md:875-883 of the reference).
 
 Inputs are shapes only (no ``seq_lens`` read, so no device sync):
 batch, kv heads, head_dim, page_size, ``max_pages = block_table.shape[1]``
-and the CU count.
+and the CU count.  The grid is sized to one round of resident waves
+(CUs x 4 SIMDs x the waves per SIMD the kernel is compiled for), with at
+least one 16-token block per wave of a split.
 """
 
 from __future__ import annotations
@@ -20,8 +22,12 @@ BLOCK_TOKENS = 16          # tokens per wave iteration (one MFMA tile)
 MAX_WAVES = 4              # waves per phase-1 workgroup
 MAX_SPLITS = 1024          # PAD_MAX_SPLITS
 MERGE_LDS_BUDGET = 48 * 1024
-TARGET_GROUPS_PER_CU = 4   # phase-1 workgroups per CU the heuristic aims at
-MIN_BLOCKS_PER_SPLIT = 4   # never split below this many 16-token blocks
+MIN_BLOCKS_PER_SPLIT = 4   # never split below this many 16-token blocks (one per wave)
+
+
+def phase1_waves_per_simd(head_dim: int) -> int:
+    """Waves per SIMD the MFMA phase-1 kernel is compiled for (amdgpu_waves_per_eu)."""
+    return 3 if head_dim <= 128 else 1
 
 
 @dataclass(frozen=True)
@@ -50,7 +56,8 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
         pps = _cdiv(mp, s)
     else:
         blocks_per_seq = _cdiv(mp * page_size, BLOCK_TOKENS)
-        want = _cdiv(TARGET_GROUPS_PER_CU * num_cus, units)
+        resident_waves = num_cus * 4 * phase1_waves_per_simd(head_dim)
+        want = resident_waves // (units * MAX_WAVES)
         cap = max(blocks_per_seq // MIN_BLOCKS_PER_SPLIT, 1)
         want = max(min(want, cap, MAX_SPLITS), 1)
         pps = _cdiv(mp, want)
@@ -60,5 +67,13 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     cap_w = max(min(MERGE_LDS_BUDGET // per_wave, MAX_WAVES), 1)
     nw = max(min(nw, cap_w), 1)
     single = s == 1
-    ws = 0 if single else batch * num_kv_heads * s * gqa * (head_dim + 2) * 4 + 256
+    ws = 0 if single else workspace_bytes(batch, num_kv_heads, gqa, head_dim, s)
     return Plan(s, pps, nw, single, ws)
+
+
+def workspace_bytes(batch: int, num_kv_heads: int, gqa: int, head_dim: int, num_splits: int) -> int:
+    """256 B alignment slack + int32 counters [B*Hkv] (256 B padded) + fp32 O [B,Hkv,S,gqa,D] + (m,l)."""
+    units = batch * num_kv_heads
+    counters = (units * 4 + 255) // 256 * 256
+    rows = units * num_splits * gqa
+    return 256 + counters + rows * head_dim * 4 + rows * 8

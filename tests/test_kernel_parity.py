@@ -255,6 +255,27 @@ def test_runs_on_current_stream():
 
 
 @pytest.mark.parametrize("engine", ENGINES)
+@pytest.mark.parametrize("num_splits", [None, 7, 64])
+def test_repeated_calls_are_bit_identical(engine, num_splits):
+    # The fused split merge runs in the last workgroup to arrive, in a fixed
+    # split order, so every call must give the same bits; a lost or doubled
+    # arrival count (or a counter left non-zero) would break this.
+    import paged_attention_decode_amd as pad
+
+    lens = [4096, 33, 2500, 1, 777, 4000]
+    bt, n = shuffled_table(lens, 16, spare_pages=2, extra_cols=1, seed=61)
+    k, v = make_cache(n, 16, 2, 128, seed=61)
+    q = torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(61))
+    args = [q.half().cuda(), k.half().cuda(), v.half().cuda(), bt.cuda(), torch.tensor(lens, dtype=torch.int32).cuda()]
+    first = pad.paged_attention_decode_ex(*args, num_splits=num_splits, engine=engine)
+    outs = [pad.paged_attention_decode_ex(*args, num_splits=num_splits, engine=engine) for _ in range(60)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o, first)
+    assert_parity(first, decode_fp16_protocol(q, k, v, bt, torch.tensor(lens, dtype=torch.int32)))
+
+
+@pytest.mark.parametrize("engine", ENGINES)
 @pytest.mark.parametrize("seed", range(FUZZ))
 def test_fuzz_shape_matrix(engine, seed):
     q, k, v, bt, sl = random_case(seed, gqa=(1, 2, 4, 6, 8), head_dims=(32, 64, 128), page_sizes=(1, 8, 16, 32),
