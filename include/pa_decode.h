@@ -32,11 +32,14 @@
  * caller's stream with no host synchronisation.  Split-K's two phases (the
  * reference's two kernels) run as one kernel launch.
  *
- * Workspace contract.  A workspace holds the fp32 split partials and one
- * int32 arrival counter per (sequence, kv head).  The counters must be zero
- * before the first launch that uses the workspace (pad_decode_workspace_init
- * or any zero-filled allocation); every launch leaves them zero again.  Two
- * launches that may run at the same time must not share a workspace (give
+ * Scratch contract.  A launch that splits sequences needs two buffers:
+ *  - `workspace` (pad_decode_workspace_bytes()): the fp32 split partials;
+ *    no state is kept in it between launches;
+ *  - `counters` (pad_decode_counters_needed() int32 entries): one arrival
+ *    counter per (sequence, kv head).  They must be zero before the first
+ *    launch that uses them (pad_decode_counters_init() or any zero-filled
+ *    allocation), and every launch leaves them zero again.
+ * Launches that may run at the same time must not share either buffer (give
  * each stream its own).
  *
  * Every entry point returns a pad_status.  Host-only functions
@@ -70,7 +73,7 @@ typedef enum pad_status {
                                     group larger than PAD_MAX_GQA          */
   PAD_ERR_STRIDE = 5,            /* head_dim stride != 1                   */
   PAD_ERR_ALIGNMENT = 6,         /* K/V/q/out rows not 16-byte aligned     */
-  PAD_ERR_WORKSPACE = 7,         /* workspace NULL or too small            */
+  PAD_ERR_WORKSPACE = 7,         /* workspace or counters NULL / too small */
   PAD_ERR_NUM_SPLITS = 8,        /* num_splits < 0 or > PAD_MAX_SPLITS     */
   PAD_ERR_LAUNCH = 9,            /* the HIP runtime rejected a launch      */
   PAD_ERR_DEVICE = 10            /* no usable device / device query failed */
@@ -102,7 +105,8 @@ typedef struct pad_decode_plan_t {
   int32_t single_pass;      /* 1: one split per sequence, no partials      */
   int32_t engine;           /* 0 = MFMA tiles, 1 = VALU/DPP dot products   */
   int32_t reserved;
-  size_t workspace_bytes;   /* counters + fp32 partials; 0 if single_pass  */
+  size_t workspace_bytes;   /* fp32 partials; 0 if single_pass             */
+  int64_t counters;         /* int32 arrival counters; 0 if single_pass    */
 } pad_decode_plan_t;
 
 /* Choose the split count and workgroup shape.  num_splits > 0 forces that
@@ -122,11 +126,17 @@ int pad_decode_plan(const pad_decode_dims* dims, int num_splits, int num_cus,
 int pad_decode_workspace_bytes(const pad_decode_dims* dims, int num_splits,
                                int num_cus, size_t* bytes);
 
-/* Zero a workspace (asynchronously, on `stream`) so its arrival counters
- * start at zero; needed once per workspace.  No counterpart in the
- * reference, whose launcher allocated fresh partials on every call. */
-int pad_decode_workspace_init(void* workspace, size_t workspace_bytes,
-                              void* stream);
+/* int32 arrival counters a launch with these arguments needs (0 when the
+ * plan is single-pass; batch * num_kv_heads otherwise).  Pure host
+ * function.  No counterpart in the reference, whose two kernel launches
+ * needed no arrival counting. */
+int pad_decode_counters_needed(const pad_decode_dims* dims, int num_splits,
+                               int num_cus, int64_t* count);
+
+/* Zero `num_counters` counters (asynchronously, on `stream`); needed once
+ * per counter buffer. */
+int pad_decode_counters_init(int32_t* counters, int64_t num_counters,
+                             void* stream);
 
 /* Launch the decode on `stream` (a hipStream_t; NULL = the null stream).
  * Asynchronous: returns once the kernels are queued.  `scale` is the
@@ -137,6 +147,7 @@ int pad_decode_workspace_init(void* workspace, size_t workspace_bytes,
 int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache,
                       const int32_t* block_table, const int32_t* seq_lens,
                       void* out, void* workspace, size_t workspace_bytes,
+                      int32_t* counters, int64_t num_counters,
                       const pad_decode_dims* dims, float scale,
                       int num_splits, void* stream);
 
@@ -149,7 +160,8 @@ int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache,
 int pad_decode_launch_ex(const void* q, const void* k_cache,
                          const void* v_cache, const int32_t* block_table,
                          const int32_t* seq_lens, void* out, void* workspace,
-                         size_t workspace_bytes, const pad_decode_dims* dims,
+                         size_t workspace_bytes, int32_t* counters,
+                         int64_t num_counters, const pad_decode_dims* dims,
                          float scale, int num_splits, int engine,
                          void* const* events, void* stream);
 

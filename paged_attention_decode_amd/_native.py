@@ -74,6 +74,7 @@ class PadPlan(ctypes.Structure):
         ("engine", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_size_t),
+        ("counters", ctypes.c_int64),
     ]
 
 
@@ -85,16 +86,21 @@ SIGNATURES = {
         [ctypes.POINTER(PadDims), ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)],
         ctypes.c_int,
     ),
+    "pad_decode_counters_needed": (
+        [ctypes.POINTER(PadDims), ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int64)],
+        ctypes.c_int,
+    ),
+    "pad_decode_counters_init": ([_VP, ctypes.c_int64, _VP], ctypes.c_int),
     "pad_decode_launch": (
-        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, ctypes.POINTER(PadDims), ctypes.c_float, ctypes.c_int, _VP],
+        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, _VP, ctypes.c_int64, ctypes.POINTER(PadDims),
+         ctypes.c_float, ctypes.c_int, _VP],
         ctypes.c_int,
     ),
     "pad_decode_launch_ex": (
-        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, ctypes.POINTER(PadDims), ctypes.c_float, ctypes.c_int,
-         ctypes.c_int, ctypes.POINTER(_VP), _VP],
+        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, _VP, ctypes.c_int64, ctypes.POINTER(PadDims),
+         ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_VP), _VP],
         ctypes.c_int,
     ),
-    "pad_decode_workspace_init": ([_VP, ctypes.c_size_t, _VP], ctypes.c_int),
     "pad_device_num_cus": ([ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "pad_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "pad_decode_abi_version": ([], ctypes.c_int),

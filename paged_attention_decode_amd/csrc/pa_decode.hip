@@ -685,26 +685,22 @@ static int validate_dims(const pad_decode_dims* d) {
   return PAD_OK;
 }
 
-// Workspace layout (from the first 256-byte boundary of the buffer):
-//   counters int32 [B*Hkv]            arrival counts; zero between launches
+// Workspace layout (from the first 256-byte boundary of the buffer); the
+// workspace holds no state between launches:
 //   o_part   fp32  [B, Hkv, S, gqa, D] unnormalised split outputs
 //   ml_part  fp32x2 [B, Hkv, S, gqa]   (m in base-2 units, l)
 // Returns the bytes needed (including 256 bytes of alignment slack) and,
 // when `ws` is given, the region pointers.
-static size_t workspace_layout(const pad_decode_dims* d, int S, void* ws, int** counters, float** o_part,
-                               float2** ml_part) {
+static size_t workspace_layout(const pad_decode_dims* d, int S, void* ws, float** o_part, float2** ml_part) {
   const int gqa = d->num_q_heads / d->num_kv_heads;
-  const size_t units = (size_t)d->batch * d->num_kv_heads;
-  const size_t counter_bytes = (units * sizeof(int) + 255u) & ~(size_t)255u;
-  const size_t rows = units * (size_t)S * gqa;
+  const size_t rows = (size_t)d->batch * d->num_kv_heads * (size_t)S * gqa;
   const size_t o_bytes = rows * (size_t)d->head_dim * sizeof(float);
   if (ws) {
     const uintptr_t base = ((uintptr_t)ws + 255u) & ~(uintptr_t)255u;
-    *counters = reinterpret_cast<int*>(base);
-    *o_part = reinterpret_cast<float*>(base + counter_bytes);
-    *ml_part = reinterpret_cast<float2*>(base + counter_bytes + o_bytes);
+    *o_part = reinterpret_cast<float*>(base);
+    *ml_part = reinterpret_cast<float2*>(base + o_bytes);
   }
-  return 256 + counter_bytes + o_bytes + rows * sizeof(float2);
+  return 256 + o_bytes + rows * sizeof(float2);
 }
 
 static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int engine,
@@ -754,7 +750,9 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   p->single_pass = (S == 1) ? 1 : 0;
   p->engine = engine;
   p->reserved = 0;
-  p->workspace_bytes = p->single_pass ? 0 : workspace_layout(d, S, nullptr, nullptr, nullptr, nullptr);
+  p->counters = 0;
+  p->workspace_bytes = p->single_pass ? 0 : workspace_layout(d, S, nullptr, nullptr, nullptr);
+  p->counters = p->single_pass ? 0 : (int64_t)d->batch * d->num_kv_heads;
   return PAD_OK;
 }
 
@@ -806,8 +804,9 @@ static hipError_t dispatch_phase1(const Phase1Args& a, dim3 grid, int nw, size_t
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 static int launch_impl(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
-                       void* out, void* ws, size_t ws_bytes, const pad_decode_dims* d, float scale,
-                       int num_splits, int engine, void* const* events, void* stream) {
+                       void* out, void* ws, size_t ws_bytes, int32_t* counters, int64_t num_counters,
+                       const pad_decode_dims* d, float scale, int num_splits, int engine, void* const* events,
+                       void* stream) {
   if (engine != 0 && engine != 1) return PAD_ERR_INVALID_SHAPE;
   int cus = 0;
   int st = device_cus(&cus);
@@ -826,13 +825,13 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
       (d->v_stride[0] | d->v_stride[1] | d->v_stride[2]) % 8)
     return PAD_ERR_ALIGNMENT;
   if (!plan.single_pass && (!ws || ws_bytes < plan.workspace_bytes)) return PAD_ERR_WORKSPACE;
+  if (!plan.single_pass && (!counters || num_counters < plan.counters)) return PAD_ERR_WORKSPACE;
 
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   const int S = plan.num_splits;
-  int* counters = nullptr;
   float* o_part = nullptr;
   float2* ml_part = nullptr;
-  if (!plan.single_pass) workspace_layout(d, S, ws, &counters, &o_part, &ml_part);
+  if (!plan.single_pass) workspace_layout(d, S, ws, &o_part, &ml_part);
 
   Phase1Args a;
   a.q = static_cast<const _Float16*>(q);
@@ -906,25 +905,36 @@ int pad_decode_workspace_bytes(const pad_decode_dims* dims, int num_splits, int 
   return PAD_OK;
 }
 
+int pad_decode_counters_needed(const pad_decode_dims* dims, int num_splits, int num_cus, int64_t* count) {
+  if (!count) return PAD_ERR_NULL_POINTER;
+  pad_decode_plan_t p;
+  const int st = pad::plan_impl(dims, num_splits, num_cus, 0, &p);
+  if (st != PAD_OK) return st;
+  *count = p.counters;
+  return PAD_OK;
+}
+
 int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                       const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
-                      const pad_decode_dims* dims, float scale, int num_splits, void* stream) {
-  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, out, workspace, workspace_bytes, dims,
-                          scale, num_splits, 0, nullptr, stream);
+                      int32_t* counters, int64_t num_counters, const pad_decode_dims* dims, float scale,
+                      int num_splits, void* stream) {
+  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, out, workspace, workspace_bytes, counters,
+                          num_counters, dims, scale, num_splits, 0, nullptr, stream);
 }
 
 int pad_decode_launch_ex(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                          const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
-                         const pad_decode_dims* dims, float scale, int num_splits, int engine,
-                         void* const* events, void* stream) {
-  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, out, workspace, workspace_bytes, dims,
-                          scale, num_splits, engine, events, stream);
+                         int32_t* counters, int64_t num_counters, const pad_decode_dims* dims, float scale,
+                         int num_splits, int engine, void* const* events, void* stream) {
+  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, out, workspace, workspace_bytes, counters,
+                          num_counters, dims, scale, num_splits, engine, events, stream);
 }
 
-int pad_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
-  if (!workspace) return PAD_ERR_NULL_POINTER;
-  if (workspace_bytes == 0) return PAD_OK;
-  return hipMemsetAsync(workspace, 0, workspace_bytes, reinterpret_cast<hipStream_t>(stream)) == hipSuccess
+int pad_decode_counters_init(int32_t* counters, int64_t num_counters, void* stream) {
+  if (!counters) return PAD_ERR_NULL_POINTER;
+  if (num_counters <= 0) return PAD_OK;
+  return hipMemsetAsync(counters, 0, (size_t)num_counters * sizeof(int32_t), reinterpret_cast<hipStream_t>(stream)) ==
+                 hipSuccess
              ? PAD_OK
              : PAD_ERR_LAUNCH;
 }
@@ -944,7 +954,8 @@ const char* pad_status_string(int status) {
       return "unsupported GQA group (num_q_heads must be a multiple of num_kv_heads, ratio <= 16)";
     case PAD_ERR_STRIDE: return "head_dim must be contiguous (stride 1) for q, k_cache, v_cache and out";
     case PAD_ERR_ALIGNMENT: return "q/k_cache/v_cache/out rows must be 16-byte aligned";
-    case PAD_ERR_WORKSPACE: return "workspace is NULL or smaller than pad_decode_workspace_bytes()";
+    case PAD_ERR_WORKSPACE:
+      return "workspace/counters NULL or smaller than pad_decode_workspace_bytes()/pad_decode_counters_needed()";
     case PAD_ERR_NUM_SPLITS: return "num_splits must be in [0, 1024]";
     case PAD_ERR_LAUNCH: return "kernel launch failed";
     case PAD_ERR_DEVICE: return "no usable HIP device";

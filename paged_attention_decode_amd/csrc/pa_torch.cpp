@@ -6,7 +6,8 @@
 // shapes, strides and data pointers from the tensors, allocates the output
 // from PyTorch's caching allocator, and calls
 // pad_decode_launch_ex() on PyTorch's current HIP stream of q's device, with
-// a persistent workspace per (device, stream).
+// persistent split scratch (workspace + arrival counters) per (device,
+// stream).
 // Argument errors surface as RuntimeError (the reference used TORCH_CHECK,
 // cuda/kernel_v4_split_k.cu:216-223).  No host synchronisation.
 
@@ -33,19 +34,30 @@ int cached_cus(int device) {
   return cus[device];
 }
 
-// One persistent, zero-initialised workspace per (device, stream): the
-// kernels' arrival counters must start at zero and are left at zero by every
-// launch, and launches on one stream are ordered, so reusing the buffer on
-// its stream is safe.  It grows (a fresh zeroed buffer, allocated and filled
-// on the same stream) when a call needs more.
-void* stream_workspace(const torch::Tensor& like, hipStream_t stream, size_t bytes) {
-  static std::map<std::pair<int, uintptr_t>, torch::Tensor> cache;
-  torch::Tensor& ws = cache[{like.get_device(), reinterpret_cast<uintptr_t>(stream)}];
-  if (!ws.defined() || static_cast<size_t>(ws.numel()) < bytes) {
-    const int64_t grown = static_cast<int64_t>(((bytes + (1u << 20) - 1) >> 20) << 20);
-    ws = torch::zeros({grown}, like.options().dtype(at::kByte));
+// Per (device, stream) scratch kept across calls: the fp32 partial
+// workspace (no state between launches) and the int32 arrival counters,
+// which start at zero and are left at zero by every launch.  Launches on one
+// stream are ordered, so reusing both on their stream is safe; each grows
+// (a fresh buffer, counters zero-filled, on the same stream) when a call
+// needs more.
+struct StreamScratch {
+  torch::Tensor workspace;
+  torch::Tensor counters;
+};
+
+StreamScratch& stream_scratch(const torch::Tensor& like, hipStream_t stream, size_t ws_bytes,
+                              int64_t num_counters) {
+  static std::map<std::pair<int, uintptr_t>, StreamScratch> cache;
+  StreamScratch& sc = cache[{like.get_device(), reinterpret_cast<uintptr_t>(stream)}];
+  if (!sc.workspace.defined() || static_cast<size_t>(sc.workspace.numel()) < ws_bytes) {
+    const int64_t grown = static_cast<int64_t>(((ws_bytes + (1u << 20) - 1) >> 20) << 20);
+    sc.workspace = torch::empty({grown}, like.options().dtype(at::kByte));
   }
-  return ws.data_ptr();
+  if (!sc.counters.defined() || sc.counters.numel() < num_counters) {
+    const int64_t grown = ((num_counters + 4095) / 4096) * 4096;
+    sc.counters = torch::zeros({grown}, like.options().dtype(at::kInt));
+  }
+  return sc;
 }
 
 void fill_dims(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
@@ -97,16 +109,21 @@ torch::Tensor forward_impl(torch::Tensor q, torch::Tensor k_cache, torch::Tensor
   fill_dims(q, k_cache, v_cache, block_table, seq_lens, out, &d);
 
   const int cus = cached_cus(q.get_device());
-  size_t ws_bytes = 0;
-  int st = pad_decode_workspace_bytes(&d, static_cast<int>(num_splits), cus, &ws_bytes);
+  pad_decode_plan_t plan;
+  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cus, &plan);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
   void* ws_ptr = nullptr;
-  if (ws_bytes > 0) ws_ptr = stream_workspace(q, stream, ws_bytes);
+  int32_t* counters = nullptr;
+  if (!plan.single_pass) {
+    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
+    ws_ptr = sc.workspace.data_ptr();
+    counters = sc.counters.data_ptr<int32_t>();
+  }
   st = pad_decode_launch_ex(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                             block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
-                            ws_ptr, ws_bytes, &d, static_cast<float>(scale), static_cast<int>(num_splits),
-                            static_cast<int>(engine), events, stream);
+                            ws_ptr, plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
+                            static_cast<int>(num_splits), static_cast<int>(engine), events, stream);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   return out;
 }
@@ -164,6 +181,7 @@ py::dict plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t 
   r["waves_per_group"] = p.waves_per_group;
   r["single_pass"] = p.single_pass;
   r["workspace_bytes"] = p.workspace_bytes;
+  r["counters"] = p.counters;
   return r;
 }
 

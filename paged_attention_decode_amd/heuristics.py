@@ -37,6 +37,7 @@ class Plan:
     waves_per_group: int
     single_pass: bool
     workspace_bytes: int
+    counters: int
 
 
 def _cdiv(a: int, b: int) -> int:
@@ -68,12 +69,10 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     nw = max(min(nw, cap_w), 1)
     single = s == 1
     ws = 0 if single else workspace_bytes(batch, num_kv_heads, gqa, head_dim, s)
-    return Plan(s, pps, nw, single, ws)
+    return Plan(s, pps, nw, single, ws, 0 if single else batch * num_kv_heads)
 
 
 def workspace_bytes(batch: int, num_kv_heads: int, gqa: int, head_dim: int, num_splits: int) -> int:
-    """256 B alignment slack + int32 counters [B*Hkv] (256 B padded) + fp32 O [B,Hkv,S,gqa,D] + (m,l)."""
-    units = batch * num_kv_heads
-    counters = (units * 4 + 255) // 256 * 256
-    rows = units * num_splits * gqa
-    return 256 + counters + rows * head_dim * 4 + rows * 8
+    """256 B alignment slack + fp32 O [B, Hkv, S, gqa, D] + (m, l) [B, Hkv, S, gqa]."""
+    rows = batch * num_kv_heads * num_splits * gqa
+    return 256 + rows * head_dim * 4 + rows * 8

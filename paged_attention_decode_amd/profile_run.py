@@ -1,0 +1,59 @@
+"""A short, fixed workload to run under rocprofv3.
+
+    python -m paged_attention_decode_amd.profile_run --config C2 --batch 64 --calls 50
+
+Runs a calibration copy first (``--copy-mb`` MiB read and written by
+PyTorch's copy kernel, 3 dispatches: the bytes a FETCH_SIZE / WRITE_SIZE
+counter should report for a plain stream of known size), then ``--calls``
+decode calls of the named configuration, rotating over enough distinct KV
+caches that the 256 MB Infinity Cache cannot serve repeats ("cold"), or on
+one set of inputs with ``--warm``.  Prints the per-call algorithmic bytes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import math
+
+import torch
+
+from . import paged_attention_decode_ex
+from . import workloads as wl
+
+
+def main() -> None:
+    p = argparse.ArgumentParser()
+    p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    p.add_argument("--batch", type=int, default=64)
+    p.add_argument("--calls", type=int, default=50)
+    p.add_argument("--engine", type=int, default=0)
+    p.add_argument("--num-splits", type=int, default=0)
+    p.add_argument("--copy-mb", type=int, default=256)
+    p.add_argument("--warm", action="store_true")
+    a = p.parse_args()
+
+    if a.copy_mb > 0:
+        n = a.copy_mb * (1 << 20) // 2
+        src = torch.randn(n, device="cuda", dtype=torch.float16)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"calibration copy: {a.copy_mb} MiB read + {a.copy_mb} MiB written per dispatch", flush=True)
+        del src, dst
+
+    w0 = wl.make(a.config, batch=a.batch, seed=1)
+    n_sets = 1 if a.warm else max(2, math.ceil(512 * (1 << 20) / (w0.k_cache.numel() * 4)) + 1)
+    sets = [w0] + [wl.make(a.config, batch=a.batch, seed=1 + i) for i in range(1, n_sets)]
+    torch.cuda.synchronize()
+    for i in range(a.calls):
+        w = sets[i % n_sets]
+        paged_attention_decode_ex(*w.args(), num_splits=a.num_splits or None, engine=a.engine)
+    torch.cuda.synchronize()
+    print(f"{w0.name}: {a.calls} calls over {n_sets} input set(s); algorithmic bytes/call {wl.bytes_of(w0)}",
+          flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -80,12 +80,17 @@ def test_plan_matches_python_mirror(batch, hq, hkv, d, ps, max_pages, splits, cu
     p = _native.PadPlan()
     assert lib.pad_decode_plan(ctypes.byref(_dims(batch, hq, hkv, d, ps, max_pages)), splits, cus, ctypes.byref(p)) == 0
     m = heuristics.plan(batch, hq, hkv, d, ps, max_pages, splits, cus)
-    assert (p.num_splits, p.pages_per_split, p.waves_per_group, bool(p.single_pass), p.workspace_bytes) == (
-        m.num_splits, m.pages_per_split, m.waves_per_group, m.single_pass, m.workspace_bytes)
+    assert (p.num_splits, p.pages_per_split, p.waves_per_group, bool(p.single_pass), p.workspace_bytes,
+            p.counters) == (m.num_splits, m.pages_per_split, m.waves_per_group, m.single_pass, m.workspace_bytes,
+                            m.counters)
     ws = ctypes.c_size_t()
     assert lib.pad_decode_workspace_bytes(ctypes.byref(_dims(batch, hq, hkv, d, ps, max_pages)), splits, cus,
                                           ctypes.byref(ws)) == 0
     assert ws.value == m.workspace_bytes
+    nc = ctypes.c_int64()
+    assert lib.pad_decode_counters_needed(ctypes.byref(_dims(batch, hq, hkv, d, ps, max_pages)), splits, cus,
+                                          ctypes.byref(nc)) == 0
+    assert nc.value == m.counters
 
 
 def test_heuristic_properties():
@@ -129,14 +134,17 @@ def test_plan_rejects_bad_strides_and_splits():
 
 # --------------------------------------------------------------------- GPU ---
 
-def _launch(lib, q, k, v, bt, sl, out, ws, dm, scale, splits, engine=None, stream=None, events=None):
+def _launch(lib, q, k, v, bt, sl, out, ws, dm, scale, splits, engine=None, stream=None, events=None, counters=None):
     wsp = ws.data_ptr() if ws is not None else None
     wsb = ws.numel() if ws is not None else 0
+    cp = counters.data_ptr() if counters is not None else None
+    cn = counters.numel() if counters is not None else 0
     if engine is None:
         return lib.pad_decode_launch(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr(),
-                                     out.data_ptr(), wsp, wsb, ctypes.byref(dm), scale, splits, stream)
+                                     out.data_ptr(), wsp, wsb, cp, cn, ctypes.byref(dm), scale, splits, stream)
     return lib.pad_decode_launch_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), bt.data_ptr(), sl.data_ptr(),
-                                    out.data_ptr(), wsp, wsb, ctypes.byref(dm), scale, splits, engine, events, stream)
+                                    out.data_ptr(), wsp, wsb, cp, cn, ctypes.byref(dm), scale, splits, engine, events,
+                                    stream)
 
 
 @pytest.mark.gpu
@@ -156,22 +164,26 @@ def test_launch_through_c_abi(splits):
     out = torch.empty_like(qd)
     dm = _native.dims_for(qd, kd, vd, btd, sld, out)
     wsb = ctypes.c_size_t()
+    nc = ctypes.c_int64()
     assert lib.pad_decode_workspace_bytes(ctypes.byref(dm), splits, 0, ctypes.byref(wsb)) == 0
-    ws = torch.full((max(wsb.value, 1),), 0x7F, dtype=torch.uint8, device="cuda")
+    assert lib.pad_decode_counters_needed(ctypes.byref(dm), splits, 0, ctypes.byref(nc)) == 0
+    assert nc.value in (0, 8)
+    # The workspace keeps no state: fill it with garbage before every launch.
+    ws = torch.empty(max(wsb.value, 1), dtype=torch.uint8, device="cuda")
+    counters = torch.full((max(nc.value, 1),), 12345, dtype=torch.int32, device="cuda")
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
-    assert lib.pad_decode_workspace_init(ws.data_ptr(), ws.numel(), stream.cuda_stream) == 0
+    assert lib.pad_decode_counters_init(counters.data_ptr(), counters.numel(), stream.cuda_stream) == 0
     for _ in range(3):  # the counters come back to zero after every launch
         out.fill_(float("nan"))
+        ws.fill_(0x7F)
         torch.cuda.synchronize()
-        st = _launch(lib, qd, kd, vd, btd, sld, out, ws, dm, 1.0 / 128 ** 0.5, splits, stream=stream.cuda_stream)
+        st = _launch(lib, qd, kd, vd, btd, sld, out, ws, dm, 1.0 / 128 ** 0.5, splits, stream=stream.cuda_stream,
+                     counters=counters)
         assert st == 0, lib.pad_status_string(st)
         stream.synchronize()
         assert_parity(out, expected)
-        if wsb.value:
-            base = (ws.data_ptr() + 255) // 256 * 256 - ws.data_ptr()
-            counters = ws[base:base + 4 * 4 * 2].view(torch.int32)
-            assert torch.all(counters == 0), counters
+        assert torch.all(counters == 0), counters
 
 
 @pytest.mark.gpu
@@ -189,14 +201,15 @@ def test_launch_ex_events_and_engines():
     for engine in (0, 1):
         out = torch.empty_like(qd)
         dm = _native.dims_for(qd, kd, vd, btd, sld, out)
-        ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+        ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+        counters = torch.zeros(64, dtype=torch.int32, device="cuda")
         evs = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         arr = (ctypes.c_void_p * 3)(*[e.cuda_event for e in evs])
         for e in evs:  # events must exist on the device before the library records them
             e.record()
         torch.cuda.synchronize()
         st = _launch(lib, qd, kd, vd, btd, sld, out, ws, dm, 1.0 / 128 ** 0.5, 4, engine=engine,
-                     stream=torch.cuda.current_stream().cuda_stream, events=arr)
+                     stream=torch.cuda.current_stream().cuda_stream, events=arr, counters=counters)
         assert st == 0, lib.pad_status_string(st)
         torch.cuda.synchronize()
         assert evs[0].elapsed_time(evs[1]) > 0.0
@@ -213,19 +226,23 @@ def test_launch_rejects_bad_arguments_without_launching():
     sl = torch.full((1,), 40, dtype=torch.int32, device="cuda")
     out = torch.empty_like(q)
     dm = _native.dims_for(q, k, k, bt, sl, out)
-    # Workspace missing for a split launch.
+    # Workspace or counters missing for a split launch.
     assert _launch(lib, q, k, k, bt, sl, out, None, dm, 0.1, 4) == 7
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    assert _launch(lib, q, k, k, bt, sl, out, ws, dm, 0.1, 4) == 7
+    assert _launch(lib, q, k, k, bt, sl, out, ws, dm, 0.1, 4, counters=torch.zeros(1, dtype=torch.int32,
+                                                                                      device="cuda")) == 7
     # Misaligned output row.
     flat = torch.empty(12 * 128 + 8, dtype=torch.float16, device="cuda")
     bad_out = flat[1:1 + 12 * 128].view(1, 12, 128)
     assert lib.pad_decode_launch(q.data_ptr(), k.data_ptr(), k.data_ptr(), bt.data_ptr(), sl.data_ptr(),
-                                 bad_out.data_ptr(), None, 0, ctypes.byref(dm), 0.1, 1, None) == 6
+                                 bad_out.data_ptr(), None, 0, None, 0, ctypes.byref(dm), 0.1, 1, None) == 6
     # Null pointer.
     assert lib.pad_decode_launch(None, k.data_ptr(), k.data_ptr(), bt.data_ptr(), sl.data_ptr(),
-                                 out.data_ptr(), None, 0, ctypes.byref(dm), 0.1, 1, None) == 1
+                                 out.data_ptr(), None, 0, None, 0, ctypes.byref(dm), 0.1, 1, None) == 1
     # VALU engine does not cover a group of 16.
     q16 = torch.zeros(1, 32, 128, dtype=torch.float16, device="cuda")
     dm16 = _native.dims_for(q16, k, k, bt, sl, torch.empty_like(q16))
     assert lib.pad_decode_launch_ex(q16.data_ptr(), k.data_ptr(), k.data_ptr(), bt.data_ptr(), sl.data_ptr(),
-                                    q16.data_ptr(), None, 0, ctypes.byref(dm16), 0.1, 1, 1, None, None) == 4
+                                    q16.data_ptr(), None, 0, None, 0, ctypes.byref(dm16), 0.1, 1, 1, None, None) == 4
     torch.cuda.synchronize()

@@ -254,6 +254,26 @@ def test_runs_on_current_stream():
         assert_parity(o, expected)
 
 
+def test_mixed_call_shapes_share_scratch():
+    # Calls of different shapes reuse the binding's per-stream scratch: a call
+    # with few long sequences (many partials) followed by calls with many
+    # sequences (many arrival counters) must each stay correct.
+    import paged_attention_decode_amd as pad
+
+    cases = []
+    for lens, seed in (([4000, 3000], 71), ([300] * 100, 72), ([1500] * 7, 73), ([64] * 300, 74)):
+        bt, n = shuffled_table(lens, 16, spare_pages=1, extra_cols=0, seed=seed)
+        k, v = make_cache(n, 16, 2, 128, seed=seed)
+        q = torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(seed))
+        sl = torch.tensor(lens, dtype=torch.int32)
+        dev = [q.half().cuda(), k.half().cuda(), v.half().cuda(), bt.cuda(), sl.cuda()]
+        cases.append((dev, decode_fp16_protocol(q, k, v, bt, sl)))
+    for _ in range(2):
+        for dev, expected in cases + cases[::-1]:
+            for s in (None, 5):
+                assert_parity(pad.paged_attention_decode(*dev, num_splits=s), expected)
+
+
 @pytest.mark.parametrize("engine", ENGINES)
 @pytest.mark.parametrize("num_splits", [None, 7, 64])
 def test_repeated_calls_are_bit_identical(engine, num_splits):
