@@ -218,9 +218,43 @@ struct KVTile {
 
 // Engine 0: MFMA 16x16x16 f16 tiles, two blocks in flight per wave (the
 // loads of block j+nw are issued before block j is computed).
+// Loads issued before seq_len is known, so their latency overlaps the
+// seq_lens read: the wave's Q^T operand (B of S^T = K.Q^T: row r16, head_dim
+// slots kp*32 + g*8 + [0,8)) and, with whole-page blocks, the page id of the
+// wave's first block (the column is clamped into the table; its value is
+// only used when the block exists).
+template <int D>
+struct WavePrologue {
+  h8_t qv[D / 32];
+  int phys_first;
+};
+
 template <int D, bool UNIFORM>
-__device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int b, int kvh, int t_begin,
-                                               int t_end, int nblk, int wave, int nw, int lane,
+__device__ __forceinline__ WavePrologue<D> wave_prologue(const Phase1Args& a, int b, int kvh, int s, int wave,
+                                                         int lane) {
+  WavePrologue<D> pr;
+  const int g = lane >> 4;
+  const int r16 = lane & 15;
+  const bool row_ok = r16 < a.gqa;
+  const _Float16* qrow = a.q + (int64_t)b * a.sqb + (int64_t)(kvh * a.gqa + (row_ok ? r16 : 0)) * a.sqh;
+#pragma unroll
+  for (int kp = 0; kp < D / 32; ++kp) {
+    h8_t x = *reinterpret_cast<const h8_t*>(qrow + kp * 32 + g * 8);
+    pr.qv[kp] = row_ok ? x : (h8_t)0;
+  }
+  pr.phys_first = 0;
+  if constexpr (UNIFORM) {
+    if (a.max_pages > 0) {
+      const int col = min(s * a.pps + wave / (a.ps / kBlockTokens), a.max_pages - 1);
+      pr.phys_first = __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b * a.sbb + (int64_t)col * a.sbp]);
+    }
+  }
+  return pr;
+}
+
+template <int D, bool UNIFORM>
+__device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePrologue<D>& pr, int b, int kvh,
+                                               int t_begin, int t_end, int nblk, int wave, int nw, int lane,
                                                float2* sm_ml, float* sm_o) {
   constexpr int DK = D / 32;  // 16-byte K chunks per lane per token
   constexpr int DT = D / 16;  // PV output tiles; V halves per lane per token
@@ -228,17 +262,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int b, int k
   const int g = lane >> 4;
   const int r16 = lane & 15;
   const bool row_ok = r16 < a.gqa;
-
-  // Q^T operand (B of S^T = K.Q^T): row r16, head_dim slots kp*32 + g*8 + [0,8).
-  h8_t qv[DK];
-  {
-    const _Float16* qrow = a.q + (int64_t)b * a.sqb + (int64_t)(kvh * a.gqa + (row_ok ? r16 : 0)) * a.sqh;
-#pragma unroll
-    for (int kp = 0; kp < DK; ++kp) {
-      h8_t x = *reinterpret_cast<const h8_t*>(qrow + kp * 32 + g * 8);
-      qv[kp] = row_ok ? x : (h8_t)0;
-    }
-  }
+  const h8_t* qv = pr.qv;
 
   float m_run = kNegInf;
   float l_run = 0.f;
@@ -264,7 +288,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int b, int k
       const int jp = jb / blocks_per_page;
       const int page = p_first + jp;
       const int slot0 = (jb - jp * blocks_per_page) * kBlockTokens;
-      const int phys = clamp_page(__builtin_amdgcn_readfirstlane(bt_row[(int64_t)page * a.sbp]), a.num_pages);
+      const int raw = jb == wave ? pr.phys_first : __builtin_amdgcn_readfirstlane(bt_row[(int64_t)page * a.sbp]);
+      const int phys = clamp_page(raw, a.num_pages);
       const char* kb = k_head + ((int64_t)phys * a.skp + (int64_t)slot0 * a.sks) * 2;
       const char* vb = v_head + ((int64_t)phys * a.svp + (int64_t)slot0 * a.svs) * 2;
 #pragma unroll
@@ -547,6 +572,8 @@ void pad_phase1_kernel(const Phase1Args a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
+  WavePrologue<D> pr;
+  if constexpr (ENGINE == 0) pr = wave_prologue<D, UNIFORM>(a, b, kvh, s, wave, lane);
   const int L = max(a.sl[(int64_t)b * a.ssl], 0);
   const int npages = min((L + a.ps - 1) / a.ps, a.max_pages);
   const int nsplit = (npages + a.pps - 1) / a.pps;  // non-empty splits of this sequence
@@ -568,7 +595,7 @@ void pad_phase1_kernel(const Phase1Args a) {
   const int nblk = (t_end - t_begin + kBlockTokens - 1) / kBlockTokens;
 
   if constexpr (ENGINE == 0) {
-    wave_loop_mfma<D, UNIFORM>(a, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o);
+    wave_loop_mfma<D, UNIFORM>(a, pr, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o);
   } else {
     wave_loop_valu<D, UNIFORM, GQA_T>(a, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o);
   }
@@ -721,20 +748,23 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     S = num_splits;
     pps = ceil_div(max_pages, S);
   } else {
-    // Heuristic: one round of resident waves.  The grid (batch x kv heads x
-    // splits workgroups of kMaxWaves waves) is sized to the waves the CUs
-    // hold at once for this kernel, so no workgroup waits for a second
-    // round, and a split never has fewer than kMinBlocks 16-token blocks
-    // (one per wave), which also bounds the fp32 partial traffic.
-    const int kMinBlocks = kMaxWaves;
-    const int64_t resident_waves = (int64_t)num_cus * 4 * phase1_waves_per_simd(d->head_dim, 0);
+    // Heuristic (fitted to measured C2 sweeps on MI355X): about two
+    // workgroups per CU (kMaxWaves waves each, well inside one round of
+    // resident waves), a power-of-two split count so the splits of a
+    // power-of-two page count are equal, and at least kMinBlocks 16-token
+    // blocks per split - 16 (four per wave) so each workgroup's fixed
+    // costs (q load, wave merge, partial publish) stay small against its
+    // streaming, or 8 for batches whose total work is a few hundred blocks,
+    // where latency, not bandwidth, sets the time.
+    const int64_t target_groups = 2 * (int64_t)num_cus;
     const int64_t blocks_per_seq = ((int64_t)max_pages * d->page_size + kBlockTokens - 1) / kBlockTokens;
-    int64_t s_want = resident_waves / (units * kMaxWaves);
+    const int64_t kMinBlocks = units * blocks_per_seq <= 4 * (int64_t)num_cus ? 8 : 16;
+    int64_t s_want = 1;
+    while (s_want * 2 * units <= target_groups) s_want *= 2;
     int64_t s_cap = blocks_per_seq / kMinBlocks;
     if (s_cap < 1) s_cap = 1;
     if (s_want > s_cap) s_want = s_cap;
     if (s_want > PAD_MAX_SPLITS) s_want = PAD_MAX_SPLITS;
-    if (s_want < 1) s_want = 1;
     pps = ceil_div(max_pages, s_want);
     S = ceil_div(max_pages, pps);
   }

@@ -9,9 +9,10 @@ large batches (profiles/notes.md:875-883 of the reference).
 
 Inputs are shapes only (no ``seq_lens`` read, so no device sync):
 batch, kv heads, head_dim, page_size, ``max_pages = block_table.shape[1]``
-and the CU count.  The grid is sized to one round of resident waves
-(CUs x 4 SIMDs x the waves per SIMD the kernel is compiled for), with at
-least one 16-token block per wave of a split.
+and the CU count.  Fitted to measured split-count sweeps of configuration
+C2 on MI355X: about two workgroups per CU (well inside one round of
+resident waves), a power-of-two split count, and at least 16 blocks of 16
+tokens per split (8 when the whole batch is only a few hundred blocks).
 """
 
 from __future__ import annotations
@@ -22,12 +23,6 @@ BLOCK_TOKENS = 16          # tokens per wave iteration (one MFMA tile)
 MAX_WAVES = 4              # waves per phase-1 workgroup
 MAX_SPLITS = 1024          # PAD_MAX_SPLITS
 MERGE_LDS_BUDGET = 48 * 1024
-MIN_BLOCKS_PER_SPLIT = 4   # never split below this many 16-token blocks (one per wave)
-
-
-def phase1_waves_per_simd(head_dim: int) -> int:
-    """Waves per SIMD the MFMA phase-1 kernel is compiled for (amdgpu_waves_per_eu)."""
-    return 3 if head_dim <= 128 else 1
 
 
 @dataclass(frozen=True)
@@ -57,9 +52,11 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
         pps = _cdiv(mp, s)
     else:
         blocks_per_seq = _cdiv(mp * page_size, BLOCK_TOKENS)
-        resident_waves = num_cus * 4 * phase1_waves_per_simd(head_dim)
-        want = resident_waves // (units * MAX_WAVES)
-        cap = max(blocks_per_seq // MIN_BLOCKS_PER_SPLIT, 1)
+        min_blocks = 8 if units * blocks_per_seq <= 4 * num_cus else 16
+        want = 1
+        while want * 2 * units <= 2 * num_cus:
+            want *= 2
+        cap = max(blocks_per_seq // min_blocks, 1)
         want = max(min(want, cap, MAX_SPLITS), 1)
         pps = _cdiv(mp, want)
         s = _cdiv(mp, pps)
