@@ -212,9 +212,17 @@ __device__ __forceinline__ int clamp_page(int phys, int64_t num_pages) {
 // One 16-token block of K and V in registers, in the MFMA operand layouts.
 template <int D>
 struct KVTile {
-  h8_t k[D / 32];       // K[token r16][kp*32 + g*8 + 0..7]
+  HVec<D / 32> k[4];    // K[token 4g+i][r16*(D/16) + 0..D/16-1]
   HVec<D / 32> v[4];    // V[token 4g+i][r16*(D/16) + 0..D/16-1]
 };
+
+// Bytes per token row of a wave's K staging tile in LDS (16 rows): the row
+// plus 16 bytes of padding, so the 16-row column reads of the MFMA operand
+// fall in different banks.
+template <int D>
+constexpr int k_stage_row_bytes() { return D * 2 + 16; }
+template <int D>
+constexpr int k_stage_bytes() { return 16 * k_stage_row_bytes<D>(); }
 
 // Engine 0: MFMA 16x16x16 f16 tiles, two blocks in flight per wave (the
 // loads of block j+nw are issued before block j is computed).
@@ -255,7 +263,7 @@ __device__ __forceinline__ WavePrologue<D> wave_prologue(const Phase1Args& a, in
 template <int D, bool UNIFORM>
 __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePrologue<D>& pr, int b, int kvh,
                                                int t_begin, int t_end, int nblk, int wave, int nw, int lane,
-                                               float2* sm_ml, float* sm_o) {
+                                               float2* sm_ml, float* sm_o, char* k_stage) {
   constexpr int DK = D / 32;  // 16-byte K chunks per lane per token
   constexpr int DT = D / 16;  // PV output tiles; V halves per lane per token
   constexpr int NDW = DT / 2;
@@ -274,10 +282,17 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePr
   const char* v_head = reinterpret_cast<const char*>(a.v + (int64_t)kvh * a.svh);
   const int32_t* bt_row = a.bt + (int64_t)b * a.sbb;
   // Lane byte offsets inside a 16-token slab of one page (loop invariant).
-  const uint32_t koff = (uint32_t)(((int64_t)r16 * a.sks + g * 8) * 2);
-  uint32_t voff[4];
+  // K and V are both read as whole token rows: lane (g, r16) reads row
+  // 4g+i, head_dim slice r16*DT, so one load instruction covers four full
+  // rows (contiguous 256 B each at head_dim 128).  K then goes through LDS
+  // into the MFMA operand layout (token per lane%16).
+  uint32_t koff[4], voff[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((int64_t)(4 * g + i) * a.svs + r16 * DT) * 2);
+  for (int i = 0; i < 4; ++i) {
+    koff[i] = (uint32_t)(((int64_t)(4 * g + i) * a.sks + r16 * DT) * 2);
+    voff[i] = (uint32_t)(((int64_t)(4 * g + i) * a.svs + r16 * DT) * 2);
+  }
+  constexpr int KROW = k_stage_row_bytes<D>();
   const int blocks_per_page = a.ps / kBlockTokens;  // UNIFORM only
   const int p_first = t_begin / a.ps;
 
@@ -293,27 +308,22 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePr
       const char* kb = k_head + ((int64_t)phys * a.skp + (int64_t)slot0 * a.sks) * 2;
       const char* vb = v_head + ((int64_t)phys * a.svp + (int64_t)slot0 * a.svs) * 2;
 #pragma unroll
-      for (int kp = 0; kp < DK; ++kp) t.k[kp] = __builtin_nontemporal_load(reinterpret_cast<const h8_t*>(kb + koff + kp * 64));
+      for (int i = 0; i < 4; ++i) t.k[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(kb + koff[i]));
 #pragma unroll
       for (int i = 0; i < 4; ++i) t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(vb + voff[i]));
     } else {
       // Any page size: each token looks up its own page; tokens past the
       // end are clamped to the last valid token (and masked in compute).
       const int t0 = t_begin + jb * kBlockTokens;
-      {
-        const int tk = min(t0 + r16, t_end - 1);
-        const int page = tk / a.ps;
-        const int phys = clamp_page(bt_row[(int64_t)page * a.sbp], a.num_pages);
-        const char* kr = k_head + ((int64_t)phys * a.skp + (int64_t)(tk - page * a.ps) * a.sks + g * 8) * 2;
-#pragma unroll
-        for (int kp = 0; kp < DK; ++kp) t.k[kp] = __builtin_nontemporal_load(reinterpret_cast<const h8_t*>(kr + kp * 64));
-      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tv = min(t0 + 4 * g + i, t_end - 1);
         const int page = tv / a.ps;
         const int phys = clamp_page(bt_row[(int64_t)page * a.sbp], a.num_pages);
-        const char* vr = v_head + ((int64_t)phys * a.svp + (int64_t)(tv - page * a.ps) * a.svs + r16 * DT) * 2;
+        const int64_t slot = tv - page * a.ps;
+        const char* kr = k_head + ((int64_t)phys * a.skp + slot * a.sks + r16 * DT) * 2;
+        const char* vr = v_head + ((int64_t)phys * a.svp + slot * a.svs + r16 * DT) * 2;
+        t.k[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(kr));
         t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(vr));
       }
     }
@@ -322,12 +332,26 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePr
   auto compute = [&](KVTile<D>& t, int jb) {
     const int t0 = t_begin + jb * kBlockTokens;
     const bool full = t0 + kBlockTokens <= t_end;
+    // K rows -> LDS (row 4g+i, slice r16*DT), then the MFMA A operand back
+    // out: lane (g, r16) takes token r16, head_dim kp*32 + g*8 + [0, 8).
+    // LDS accesses of one wave complete in order, so the reads see the
+    // writes, and the next block's writes follow these reads.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(k_stage + (4 * g + i) * KROW + r16 * DT * 2);
+#pragma unroll
+      for (int w = 0; w < NDW; ++w) dst[w] = t.k[i].w[w];
+    }
+    h8_t kk[DK];
+#pragma unroll
+    for (int kp = 0; kp < DK; ++kp)
+      kk[kp] = *reinterpret_cast<const h8_t*>(k_stage + r16 * KROW + (kp * 32 + g * 8) * 2);
     // S^T[token 4g+i][row r16] over head_dim.
     f4_t sacc = (f4_t)0.f;
 #pragma unroll
     for (int kp = 0; kp < DK; ++kp) {
-      const h4_t k_lo = __builtin_shufflevector(t.k[kp], t.k[kp], 0, 1, 2, 3);
-      const h4_t k_hi = __builtin_shufflevector(t.k[kp], t.k[kp], 4, 5, 6, 7);
+      const h4_t k_lo = __builtin_shufflevector(kk[kp], kk[kp], 0, 1, 2, 3);
+      const h4_t k_hi = __builtin_shufflevector(kk[kp], kk[kp], 4, 5, 6, 7);
       const h4_t q_lo = __builtin_shufflevector(qv[kp], qv[kp], 0, 1, 2, 3);
       const h4_t q_hi = __builtin_shufflevector(qv[kp], qv[kp], 4, 5, 6, 7);
       sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k_lo, q_lo, sacc, 0, 0, 0);
@@ -565,6 +589,8 @@ void pad_phase1_kernel(const Phase1Args a) {
   float2* sm_ml = reinterpret_cast<float2*>(smem_f4);  // [nw][16]
   const int nw = blockDim.x >> 6;
   float* sm_o = reinterpret_cast<float*>(smem_f4) + nw * 32;  // [nw][gqa][D]
+  // [nw] K staging tiles (MFMA engine), after the wave states.
+  char* k_stage_all = reinterpret_cast<char*>(sm_o + nw * a.gqa * D);
 
   const int s = blockIdx.x;
   const int kvh = blockIdx.y;
@@ -595,7 +621,8 @@ void pad_phase1_kernel(const Phase1Args a) {
   const int nblk = (t_end - t_begin + kBlockTokens - 1) / kBlockTokens;
 
   if constexpr (ENGINE == 0) {
-    wave_loop_mfma<D, UNIFORM>(a, pr, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o);
+    wave_loop_mfma<D, UNIFORM>(a, pr, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o,
+                               k_stage_all + wave * k_stage_bytes<D>());
   } else {
     wave_loop_valu<D, UNIFORM, GQA_T>(a, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o);
   }
@@ -896,7 +923,10 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.scale_log2 = scale * kLog2e;
 
   const int nw = plan.waves_per_group;
-  const size_t lds = (size_t)nw * 16 * sizeof(float2) + (size_t)nw * gqa * d->head_dim * sizeof(float);
+  // Dynamic LDS: wave (m, l) [nw][16], wave O [nw][gqa][D], and for the MFMA
+  // engine one padded 16-row K staging tile per wave.
+  const size_t k_stage = engine == 0 ? (size_t)nw * 16 * (d->head_dim * 2 + 16) : 0;
+  const size_t lds = (size_t)nw * 16 * sizeof(float2) + (size_t)nw * gqa * d->head_dim * sizeof(float) + k_stage;
   const dim3 grid1(S, d->num_kv_heads, d->batch);
 
   if (events && events[0] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[0]), hs) != hipSuccess)
