@@ -59,7 +59,7 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBlockTokens = 16;  // tokens per wave iteration (one MFMA tile)
-constexpr int kMaxWaves = 4;
+constexpr int kMaxWaves = 8;
 constexpr int kMergeLdsBudget = 48 * 1024;  // bytes of LDS for the wave merge
 // Headroom (base-2 units) a score may exceed the running reference max before
 // the accumulators are rescaled; fp16 weights stay <= 2^8.
@@ -196,6 +196,15 @@ __device__ __forceinline__ float2 load_device_f2(__amdgpu_buffer_rsrc_t r, uint3
   return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCachePolicyDevice));
 }
 
+// Reads an int32 at a wave-uniform address with a scalar load (constant
+// address space): the value lands in an SGPR and its wait counts on the
+// LDS/scalar counter, so it never has to drain the K/V vector loads in
+// flight, as a vector load of the same word would (vector loads complete in
+// order).  The memory must stay unchanged while the kernel runs.
+__device__ __forceinline__ int32_t load_uniform_i32(const int32_t* p) {
+  return *(const __attribute__((address_space(4))) int32_t*)p;
+}
+
 __device__ __forceinline__ int clamp_page(int phys, int64_t num_pages) {
   // Keeps every access inside the cache for an invalid block_table entry
   // (the reference documents valid ids as a precondition and does not
@@ -254,7 +263,7 @@ __device__ __forceinline__ WavePrologue<D> wave_prologue(const Phase1Args& a, in
   if constexpr (UNIFORM) {
     if (a.max_pages > 0) {
       const int col = min(s * a.pps + wave / (a.ps / kBlockTokens), a.max_pages - 1);
-      pr.phys_first = __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b * a.sbb + (int64_t)col * a.sbp]);
+      pr.phys_first = load_uniform_i32(a.bt + (int64_t)b * a.sbb + (int64_t)col * a.sbp);
     }
   }
   return pr;
@@ -296,15 +305,21 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePr
   const int blocks_per_page = a.ps / kBlockTokens;  // UNIFORM only
   const int p_first = t_begin / a.ps;
 
+  // UNIFORM: raw page id of the block the next load() reads.  Each load()
+  // consumes it and issues the scalar read of the following block's id, so
+  // that read is in flight during a whole compute() (calls come in block
+  // order wave, wave+nw, ...; past the split the last block's id is reread).
+  int pid_next = pr.phys_first;
+
   auto load = [&](KVTile<D>& t, int jb) {
     if constexpr (UNIFORM) {
       // page_size % 16 == 0 and splits start on page boundaries: the block
       // lives in one page, so its page id and base address are wave-uniform.
       const int jp = jb / blocks_per_page;
-      const int page = p_first + jp;
       const int slot0 = (jb - jp * blocks_per_page) * kBlockTokens;
-      const int raw = jb == wave ? pr.phys_first : __builtin_amdgcn_readfirstlane(bt_row[(int64_t)page * a.sbp]);
-      const int phys = clamp_page(raw, a.num_pages);
+      const int phys = clamp_page(pid_next, a.num_pages);
+      const int page_after = p_first + min(jb + nw, nblk - 1) / blocks_per_page;
+      pid_next = load_uniform_i32(bt_row + (int64_t)page_after * a.sbp);
       const char* kb = k_head + ((int64_t)phys * a.skp + (int64_t)slot0 * a.sks) * 2;
       const char* vb = v_head + ((int64_t)phys * a.svp + (int64_t)slot0 * a.svs) * 2;
 #pragma unroll
@@ -481,7 +496,7 @@ __device__ __forceinline__ void wave_loop_valu(const Phase1Args& a, int b, int k
     const _Float16* vrow[4];
     if constexpr (UNIFORM) {
       const int page = t0 / a.ps;
-      const int phys = clamp_page(__builtin_amdgcn_readfirstlane(bt_row[(int64_t)page * a.sbp]), a.num_pages);
+      const int phys = clamp_page(load_uniform_i32(bt_row + (int64_t)page * a.sbp), a.num_pages);
       const int slot0 = t0 - page * a.ps;
       const _Float16* kbase = a.k + (int64_t)phys * a.skp + koff_h + (int64_t)slot0 * a.sks;
       const _Float16* vbase = a.v + (int64_t)phys * a.svp + voff_h + (int64_t)slot0 * a.svs;
@@ -583,7 +598,7 @@ constexpr int phase1_waves_per_simd(int d, int engine) {
 
 // Phase 1: one workgroup per (split, kv head, sequence).
 template <int D, bool UNIFORM, int ENGINE, int GQA_T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE))))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE))))
 void pad_phase1_kernel(const Phase1Args a) {
   extern __shared__ float4 smem_f4[];
   float2* sm_ml = reinterpret_cast<float2*>(smem_f4);  // [nw][16]
@@ -767,6 +782,15 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   const int max_pages = d->max_pages > 0 ? d->max_pages : 1;
   const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
 
+  // Regimes (fitted to measured split sweeps of C2 batch 1-64, C3 and C4 on
+  // MI355X).  Bandwidth-bound shapes run one 4-wave workgroup per CU: that
+  // streamed faster than two (batch 64: 44.0 vs 46.8 us; C4: 86 vs 94 us),
+  // and fewer, longer splits shorten the merge.  Latency-bound shapes (at
+  // most 16 blocks of work per CU) run 8-wave workgroups on at most half the
+  // CUs: fewer splits to merge, each streamed by more waves (batch 8: 11.9
+  // vs 13.2 us).
+  const int64_t blocks_per_seq = ((int64_t)max_pages * d->page_size + kBlockTokens - 1) / kBlockTokens;
+  const bool latency_bound = units * blocks_per_seq <= 16 * (int64_t)num_cus;
   int S;
   int pps;
   if (num_splits > 0) {
@@ -775,19 +799,14 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     S = num_splits;
     pps = ceil_div(max_pages, S);
   } else {
-    // Heuristic (fitted to measured C2 sweeps on MI355X): about two
-    // workgroups per CU (kMaxWaves waves each, well inside one round of
-    // resident waves), a power-of-two split count so the splits of a
-    // power-of-two page count are equal, and at least kMinBlocks 16-token
-    // blocks per split - 16 (four per wave) so each workgroup's fixed
-    // costs (q load, wave merge, partial publish) stay small against its
-    // streaming, or 8 for batches whose total work is a few hundred blocks,
-    // where latency, not bandwidth, sets the time.
-    const int64_t target_groups = 2 * (int64_t)num_cus;
-    const int64_t blocks_per_seq = ((int64_t)max_pages * d->page_size + kBlockTokens - 1) / kBlockTokens;
-    const int64_t kMinBlocks = units * blocks_per_seq <= 4 * (int64_t)num_cus ? 8 : 16;
+    // A power-of-two split count (the splits of a power-of-two page count
+    // are then equal) with at least kMinBlocks 16-token blocks per split, so
+    // each workgroup's fixed costs (q load, wave merge, partial publish)
+    // stay small against its streaming.
+    constexpr int64_t kMinBlocks = 16;
+    const int64_t max_groups = latency_bound ? num_cus / 2 : num_cus;
     int64_t s_want = 1;
-    while (s_want * 2 * units <= target_groups) s_want *= 2;
+    while (s_want * 2 * units <= max_groups) s_want *= 2;
     int64_t s_cap = blocks_per_seq / kMinBlocks;
     if (s_cap < 1) s_cap = 1;
     if (s_want > s_cap) s_want = s_cap;
@@ -795,8 +814,12 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     pps = ceil_div(max_pages, s_want);
     S = ceil_div(max_pages, pps);
   }
+  // Waves per workgroup: never more than the split has blocks or the wave
+  // merge's LDS allows.
   const int64_t split_tokens = (int64_t)pps * d->page_size;
   int nw = (int)((split_tokens + kBlockTokens - 1) / kBlockTokens);
+  const int nw_max = latency_bound ? kMaxWaves : kMaxWaves / 2;
+  if (nw > nw_max) nw = nw_max;
   const int cap = merge_wave_cap(gqa, d->head_dim);
   if (nw > cap) nw = cap;
   if (nw < 1) nw = 1;

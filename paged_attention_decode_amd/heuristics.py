@@ -9,10 +9,11 @@ large batches (profiles/notes.md:875-883 of the reference).
 
 Inputs are shapes only (no ``seq_lens`` read, so no device sync):
 batch, kv heads, head_dim, page_size, ``max_pages = block_table.shape[1]``
-and the CU count.  Fitted to measured split-count sweeps of configuration
-C2 on MI355X: about two workgroups per CU (well inside one round of
-resident waves), a power-of-two split count, and at least 16 blocks of 16
-tokens per split (8 when the whole batch is only a few hundred blocks).
+and the CU count.  Fitted to measured split-count sweeps of configurations
+C2 (batch 1-64), C3 and C4 on MI355X: a power-of-two split count with at
+least 16 blocks of 16 tokens per split; bandwidth-bound shapes get one
+4-wave workgroup per CU, latency-bound ones (at most 16 blocks of work per
+CU) 8-wave workgroups on at most half the CUs.
 """
 
 from __future__ import annotations
@@ -20,8 +21,9 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 BLOCK_TOKENS = 16          # tokens per wave iteration (one MFMA tile)
-MAX_WAVES = 4              # waves per phase-1 workgroup
+MAX_WAVES = 8              # waves per phase-1 workgroup (4 once the CUs are filled)
 MAX_SPLITS = 1024          # PAD_MAX_SPLITS
+MIN_BLOCKS = 16            # 16-token blocks per split, at least
 MERGE_LDS_BUDGET = 48 * 1024
 
 
@@ -47,20 +49,22 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     gqa = num_q_heads // num_kv_heads
     mp = max_pages if max_pages > 0 else 1
     units = max(batch, 1) * num_kv_heads
+    blocks_per_seq = _cdiv(mp * page_size, BLOCK_TOKENS)
+    latency_bound = units * blocks_per_seq <= 16 * num_cus
     if num_splits > 0:
         s = num_splits
         pps = _cdiv(mp, s)
     else:
-        blocks_per_seq = _cdiv(mp * page_size, BLOCK_TOKENS)
-        min_blocks = 8 if units * blocks_per_seq <= 4 * num_cus else 16
+        max_groups = num_cus // 2 if latency_bound else num_cus
         want = 1
-        while want * 2 * units <= 2 * num_cus:
+        while want * 2 * units <= max_groups:
             want *= 2
-        cap = max(blocks_per_seq // min_blocks, 1)
+        cap = max(blocks_per_seq // MIN_BLOCKS, 1)
         want = max(min(want, cap, MAX_SPLITS), 1)
         pps = _cdiv(mp, want)
         s = _cdiv(mp, pps)
     nw = _cdiv(pps * page_size, BLOCK_TOKENS)
+    nw = min(nw, MAX_WAVES if latency_bound else MAX_WAVES // 2)
     per_wave = 16 * 8 + gqa * head_dim * 4
     cap_w = max(min(MERGE_LDS_BUDGET // per_wave, MAX_WAVES), 1)
     nw = max(min(nw, cap_w), 1)

@@ -94,10 +94,15 @@ def test_plan_matches_python_mirror(batch, hq, hkv, d, ps, max_pages, splits, cu
 
 
 def test_heuristic_properties():
-    # Fills the chip at batch 1 without splitting below 4 blocks per split,
-    # and does not over-split large batches.
+    # Batch 1 (latency-bound): 8-wave workgroups on at most half the CUs,
+    # each split at least 16 blocks (2 per wave).  Bandwidth-bound batches:
+    # one 4-wave workgroup per CU, no more.
     p1 = heuristics.plan(1, 12, 2, 128, 16, 256)
-    assert p1.num_splits * 2 >= 64 and p1.pages_per_split * 16 >= 64
+    assert p1.waves_per_group == 8 and p1.pages_per_split * 16 >= 16 * 16
+    assert 32 <= p1.num_splits * 2 * p1.waves_per_group and p1.num_splits * 2 <= 128
+    for b in (16, 32, 64):
+        p = heuristics.plan(b, 12, 2, 128, 16, 256)
+        assert p.waves_per_group == 4 and p.num_splits * b * 2 == 256
     p64 = heuristics.plan(64, 12, 2, 128, 16, 256)
     assert p64.num_splits <= 8
     p_big = heuristics.plan(256, 64, 8, 128, 16, 2048)
