@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define PAD_ABI_VERSION 1
+#define PAD_ABI_VERSION 2
 
 /* Largest supported GQA group (query heads per KV head); the reference's
  * bound is the same (cuda/kernel_v4_split_k.cu:44). */
@@ -115,7 +115,13 @@ typedef struct pad_decode_plan_t {
  * depends only on shapes and the CU count (num_cus <= 0 means 256).  Pure
  * host function: it reads neither seq_lens nor block_table.  Replaces the
  * reference's fixed default _DEFAULT_NUM_SPLITS = 64
- * (src/kernel_cuda_v4.py:16). */
+ * (src/kernel_cuda_v4.py:16).
+ * The launch grid has G = batch * num_kv_heads * num_splits workgroups.
+ * With the heuristic (num_splits == 0), a split plan and batch <= 256, the
+ * kernel itself reads every sequence length and re-plans the G workgroups
+ * over the pages actually in use (equal page chunks, so ragged batches and
+ * sequences shorter than max_pages * page_size stay balanced); with every
+ * sequence at full capacity that plan is the static one. */
 int pad_decode_plan(const pad_decode_dims* dims, int num_splits, int num_cus,
                     pad_decode_plan_t* plan);
 
@@ -164,6 +170,26 @@ int pad_decode_launch_ex(const void* q, const void* k_cache,
                          int64_t num_counters, const pad_decode_dims* dims,
                          float scale, int num_splits, int engine,
                          void* const* events, void* stream);
+
+/* Decode over a CSR page index instead of the dense block table: the page
+ * ids of sequence b are indices[indptr[b] .. indptr[b+1]) (int32, in
+ * logical order) and its last page holds last_page_len[b] tokens, so
+ * seq_len[b] = (indptr[b+1] - indptr[b] - 1) * page_size + last_page_len[b]
+ * (0 for a sequence with no pages).  This is the (indptr, indices,
+ * last_page_len) triple the reference's FlashInfer adapter derives from the
+ * dense table (src/flashinfer_adapter.py:40-65) and hands to FlashInfer's
+ * plan/run (:100-112); here the kernel reads it directly.  In `dims`,
+ * max_pages is the number of entries in `indices`; bt_stride and sl_stride
+ * are ignored.  Workspace, counters, scale, num_splits, engine and stream
+ * are as in pad_decode_launch_ex(), and pad_decode_workspace_bytes() /
+ * pad_decode_counters_needed() size the scratch from the same dims. */
+int pad_decode_launch_csr(const void* q, const void* k_cache,
+                          const void* v_cache, const int32_t* indices,
+                          const int32_t* indptr, const int32_t* last_page_len,
+                          void* out, void* workspace, size_t workspace_bytes,
+                          int32_t* counters, int64_t num_counters,
+                          const pad_decode_dims* dims, float scale,
+                          int num_splits, int engine, void* stream);
 
 /* Compute units of the current device (cached per device). */
 int pad_device_num_cus(int* num_cus);

@@ -24,4 +24,7 @@ Contents (each function cites the reference file:line it restates):
   Pinned against ``brute`` (split invariance over many split counts,
   including empty splits), and by planted-mistake tests that show a dropped
   rescale, a dropped guard or a wrong merge index is caught.
+* ``csr`` - the dense -> CSR page-index conversion of the reference's
+  FlashInfer adapter (src/flashinfer_adapter.py:40-65) and its inverse.
+  Pinned by hand-computed known answers and round trips.
 """

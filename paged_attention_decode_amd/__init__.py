@@ -10,8 +10,10 @@ from .ops import (  # noqa: F401
     ENGINE_VALU,
     SUPPORTED_HEAD_DIMS,
     paged_attention_decode,
+    paged_attention_decode_csr,
     paged_attention_decode_cuda_v4,
     paged_attention_decode_ex,
+    paged_kv_indices,
     plan,
 )
 
@@ -19,6 +21,8 @@ __all__ = [
     "paged_attention_decode",
     "paged_attention_decode_cuda_v4",
     "paged_attention_decode_ex",
+    "paged_attention_decode_csr",
+    "paged_kv_indices",
     "plan",
     "ENGINE_MFMA",
     "ENGINE_VALU",

@@ -60,31 +60,56 @@ constexpr float kNegInf = -__builtin_inff();
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBlockTokens = 16;  // tokens per wave iteration (one MFMA tile)
 constexpr int kMaxWaves = 8;
+// Fewest 16-token blocks per split (or planned item): each workgroup's fixed
+// costs (q load, wave merge, partial publish) stay small against its streaming.
+constexpr int kMinBlocks = 16;
 constexpr int kMergeLdsBudget = 48 * 1024;  // bytes of LDS for the wave merge
 // Headroom (base-2 units) a score may exceed the running reference max before
 // the accumulators are rescaled; fp16 weights stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
 
+// Largest batch the in-kernel work planner handles (4 sequences per lane).
+constexpr int kPlanMaxBatch = 256;
+
 struct Phase1Args {
+  // Control fields first: they are read at the start of every workgroup.
+  int gqa, ps, pps, num_splits, hkv, max_pages, batch;
+  int nw;          // waves per workgroup (blockDim.x / 64)
+  int ps_shift;    // log2(ps) when ps is a power of two, else -1
+  int csr;         // 1: page ids from (indptr, indices, last_page_len)
+  int balance;     // 1: items planned from the sequence lengths in-kernel
+  int min_chunk;   // planner: fewest pages per item
+  float scale_log2;
+  const int32_t* bt;      // dense: block_table [B, max_pages]; CSR: indices
+  const int32_t* sl;      // dense: seq_lens [B]
+  const int32_t* indptr;  // CSR: [B + 1] offsets of each sequence's page ids in bt
+  const int32_t* lpl;     // CSR: [B] tokens in each sequence's last page
+  int64_t sbb, sbp;
+  int64_t ssl;
   const _Float16* q;
   const _Float16* k;
   const _Float16* v;
-  const int32_t* bt;
-  const int32_t* sl;
   _Float16* out;
-  float* o_part;   // [B, Hkv, S, gqa, D]
-  float2* ml_part; // [B, Hkv, S, gqa]  (m in base-2 units, l)
+  float* o_part;   // [G, gqa, D], one slot per workgroup of the grid
+  float2* ml_part; // [G, gqa]  (m in base-2 units, l)
   int* counters;   // [B, Hkv] arrival counts, zero between launches
   int64_t sqb, sqh;
   int64_t skp, sks, skh;
   int64_t svp, svs, svh;
-  int64_t sbb, sbp;
-  int64_t ssl;
   int64_t sob, soh;
   int64_t num_pages;
-  int gqa, ps, pps, num_splits, hkv, max_pages;
-  float scale_log2;
 };
+
+// Token -> page index, and pages covering n tokens (shift for power-of-two
+// page sizes).
+__device__ __forceinline__ int page_of(const Phase1Args& a, int t) {
+  return a.ps_shift >= 0 ? (t >> a.ps_shift) : t / a.ps;
+}
+__device__ __forceinline__ int pages_for(const Phase1Args& a, int n) { return page_of(a, n + a.ps - 1); }
+// 16-token block -> page index (page_size a multiple of 16).
+__device__ __forceinline__ int block_page(const Phase1Args& a, int jb) {
+  return a.ps_shift >= 4 ? (jb >> (a.ps_shift - 4)) : jb / (a.ps / 16);
+}
 
 __device__ __forceinline__ float exp2_fast(float x) {
   return __builtin_amdgcn_exp2f(x);  // v_exp_f32; exp2(-inf) = 0
@@ -215,8 +240,12 @@ __device__ __forceinline__ int clamp_page(int phys, int64_t num_pages) {
 
 // ---------------------------------------------------------------------------
 // Per-wave state handed to the workgroup merge, written to LDS in one format
-// for both engines:  sm_ml[w*16 + row] = (m, l),  sm_o[(w*gqa + row)*D + d].
+// for both engines:  sm_ml[w*16 + row] = (m, l),
+// sm_o[(w*gqa + row)*wave_row_floats<D>() + d].  The 16-byte row pad puts
+// the 16 rows a wave writes with one instruction in different LDS banks.
 // ---------------------------------------------------------------------------
+template <int D>
+constexpr int wave_row_floats() { return D + 4; }
 
 // One 16-token block of K and V in registers, in the MFMA operand layouts.
 template <int D>
@@ -235,51 +264,39 @@ constexpr int k_stage_bytes() { return 16 * k_stage_row_bytes<D>(); }
 
 // Engine 0: MFMA 16x16x16 f16 tiles, two blocks in flight per wave (the
 // loads of block j+nw are issued before block j is computed).
-// Loads issued before seq_len is known, so their latency overlaps the
-// seq_lens read: the wave's Q^T operand (B of S^T = K.Q^T: row r16, head_dim
-// slots kp*32 + g*8 + [0,8)) and, with whole-page blocks, the page id of the
-// wave's first block (the column is clamped into the table; its value is
-// only used when the block exists).
-template <int D>
-struct WavePrologue {
-  h8_t qv[D / 32];
-  int phys_first;
-};
-
-template <int D, bool UNIFORM>
-__device__ __forceinline__ WavePrologue<D> wave_prologue(const Phase1Args& a, int b, int kvh, int s, int wave,
-                                                         int lane) {
-  WavePrologue<D> pr;
-  const int g = lane >> 4;
-  const int r16 = lane & 15;
-  const bool row_ok = r16 < a.gqa;
-  const _Float16* qrow = a.q + (int64_t)b * a.sqb + (int64_t)(kvh * a.gqa + (row_ok ? r16 : 0)) * a.sqh;
-#pragma unroll
-  for (int kp = 0; kp < D / 32; ++kp) {
-    h8_t x = *reinterpret_cast<const h8_t*>(qrow + kp * 32 + g * 8);
-    pr.qv[kp] = row_ok ? x : (h8_t)0;
-  }
-  pr.phys_first = 0;
-  if constexpr (UNIFORM) {
-    if (a.max_pages > 0) {
-      const int col = min(s * a.pps + wave / (a.ps / kBlockTokens), a.max_pages - 1);
-      pr.phys_first = load_uniform_i32(a.bt + (int64_t)b * a.sbb + (int64_t)col * a.sbp);
-    }
-  }
-  return pr;
+// With whole-page blocks, the page id of the wave's first block is read
+// before the sequence length is known, so its latency overlaps the
+// seq_lens read (the column is clamped into the table; its value is only
+// used when the block exists).
+__device__ __forceinline__ int first_page_id(const Phase1Args& a, const int32_t* ids_row, int64_t ids_stride,
+                                             int col_max, int p_first, int wave) {
+  if (col_max < 0) return 0;
+  const int col = min(p_first + block_page(a, wave), col_max);
+  return load_uniform_i32(ids_row + (int64_t)col * ids_stride);
 }
 
 template <int D, bool UNIFORM>
-__device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePrologue<D>& pr, int b, int kvh,
-                                               int t_begin, int t_end, int nblk, int wave, int nw, int lane,
-                                               float2* sm_ml, float* sm_o, char* k_stage) {
+__device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_first, const int32_t* bt_row,
+                                               int64_t ids_stride, int b, int kvh, int t_begin, int t_end,
+                                               int nblk, int wave, int nw, int lane, float2* sm_ml, float* sm_o,
+                                               char* k_stage) {
   constexpr int DK = D / 32;  // 16-byte K chunks per lane per token
   constexpr int DT = D / 16;  // PV output tiles; V halves per lane per token
   constexpr int NDW = DT / 2;
   const int g = lane >> 4;
   const int r16 = lane & 15;
   const bool row_ok = r16 < a.gqa;
-  const h8_t* qv = pr.qv;
+  // The wave's Q^T operand (B of S^T = K.Q^T: row r16, head_dim slots
+  // kp*32 + g*8 + [0,8)), loaded after the first K/V block is in flight.
+  h8_t qv[DK];
+  auto load_q = [&]() {
+    const _Float16* qrow = a.q + (int64_t)b * a.sqb + (int64_t)(kvh * a.gqa + (row_ok ? r16 : 0)) * a.sqh;
+#pragma unroll
+    for (int kp = 0; kp < DK; ++kp) {
+      const h8_t x = *reinterpret_cast<const h8_t*>(qrow + kp * 32 + g * 8);
+      qv[kp] = row_ok ? x : (h8_t)0;
+    }
+  };
 
   float m_run = kNegInf;
   float l_run = 0.f;
@@ -289,7 +306,6 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePr
 
   const char* k_head = reinterpret_cast<const char*>(a.k + (int64_t)kvh * a.skh);
   const char* v_head = reinterpret_cast<const char*>(a.v + (int64_t)kvh * a.svh);
-  const int32_t* bt_row = a.bt + (int64_t)b * a.sbb;
   // Lane byte offsets inside a 16-token slab of one page (loop invariant).
   // K and V are both read as whole token rows: lane (g, r16) reads row
   // 4g+i, head_dim slice r16*DT, so one load instruction covers four full
@@ -302,24 +318,23 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePr
     voff[i] = (uint32_t)(((int64_t)(4 * g + i) * a.svs + r16 * DT) * 2);
   }
   constexpr int KROW = k_stage_row_bytes<D>();
-  const int blocks_per_page = a.ps / kBlockTokens;  // UNIFORM only
-  const int p_first = t_begin / a.ps;
+  const int p_first = page_of(a, t_begin);
 
   // UNIFORM: raw page id of the block the next load() reads.  Each load()
   // consumes it and issues the scalar read of the following block's id, so
   // that read is in flight during a whole compute() (calls come in block
   // order wave, wave+nw, ...; past the split the last block's id is reread).
-  int pid_next = pr.phys_first;
+  int pid_next = phys_first;
 
   auto load = [&](KVTile<D>& t, int jb) {
     if constexpr (UNIFORM) {
       // page_size % 16 == 0 and splits start on page boundaries: the block
       // lives in one page, so its page id and base address are wave-uniform.
-      const int jp = jb / blocks_per_page;
-      const int slot0 = (jb - jp * blocks_per_page) * kBlockTokens;
+      const int jp = block_page(a, jb);
+      const int slot0 = jb * kBlockTokens - jp * a.ps;
       const int phys = clamp_page(pid_next, a.num_pages);
-      const int page_after = p_first + min(jb + nw, nblk - 1) / blocks_per_page;
-      pid_next = load_uniform_i32(bt_row + (int64_t)page_after * a.sbp);
+      const int page_after = p_first + block_page(a, min(jb + nw, nblk - 1));
+      pid_next = load_uniform_i32(bt_row + (int64_t)page_after * ids_stride);
       const char* kb = k_head + ((int64_t)phys * a.skp + (int64_t)slot0 * a.sks) * 2;
       const char* vb = v_head + ((int64_t)phys * a.svp + (int64_t)slot0 * a.svs) * 2;
 #pragma unroll
@@ -333,8 +348,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePr
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tv = min(t0 + 4 * g + i, t_end - 1);
-        const int page = tv / a.ps;
-        const int phys = clamp_page(bt_row[(int64_t)page * a.sbp], a.num_pages);
+        const int page = page_of(a, tv);
+        const int phys = clamp_page(bt_row[(int64_t)page * ids_stride], a.num_pages);
         const int64_t slot = tv - page * a.ps;
         const char* kr = k_head + ((int64_t)phys * a.skp + slot * a.sks + r16 * DT) * 2;
         const char* vr = v_head + ((int64_t)phys * a.svp + slot * a.svs + r16 * DT) * 2;
@@ -426,6 +441,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePr
   if (n_mine > 0) {
     int it = 0;
     load(ta, wave);
+    load_q();
     for (; it + 2 < n_mine; it += 2) {
       load(tb, wave + (it + 1) * nw);
       compute(ta, wave + it * nw);
@@ -446,21 +462,29 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, const WavePr
   l_tot += shfl_xor_f(l_tot, 32);
   if (row_ok) {
     if (g == 0) sm_ml[wave * 16 + r16] = make_float2(m_run, l_tot);
-    // Lane owns O[row r16][g*D/4 + i*DT + dt].
-    float* dst = sm_o + (wave * a.gqa + r16) * D + g * (D / 4);
+    // Lane owns O[row r16][g*D/4 + i*DT + dt]: for each i, DT consecutive
+    // floats, written as 16- or 8-byte vectors.
+    float* dst = sm_o + (wave * a.gqa + r16) * wave_row_floats<D>() + g * (D / 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      if constexpr (DT % 4 == 0) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) dst[i * DT + dt] = o[dt][i];
+        for (int dt = 0; dt < DT; dt += 4)
+          *reinterpret_cast<f4_t*>(dst + i * DT + dt) = f4_t{o[dt][i], o[dt + 1][i], o[dt + 2][i], o[dt + 3][i]};
+      } else {
+#pragma unroll
+        for (int dt = 0; dt < DT; dt += 2)
+          *reinterpret_cast<float2*>(dst + i * DT + dt) = make_float2(o[dt][i], o[dt + 1][i]);
+      }
     }
   }
 }
 
 // Engine 1: VALU dot products with DPP row reductions.
 template <int D, bool UNIFORM, int GQA_T>
-__device__ __forceinline__ void wave_loop_valu(const Phase1Args& a, int b, int kvh, int t_begin,
-                                               int t_end, int nblk, int wave, int nw, int lane,
-                                               float2* sm_ml, float* sm_o) {
+__device__ __forceinline__ void wave_loop_valu(const Phase1Args& a, const int32_t* bt_row, int64_t ids_stride,
+                                               int b, int kvh, int t_begin, int t_end, int nblk, int wave,
+                                               int nw, int lane, float2* sm_ml, float* sm_o) {
   constexpr int DT = D / 16;  // halves per lane per token
   constexpr int NDW = DT / 2;
   const int g = lane >> 4;    // token group: tokens 4g+i of each block
@@ -488,15 +512,14 @@ __device__ __forceinline__ void wave_loop_valu(const Phase1Args& a, int b, int k
 
   const int64_t koff_h = (int64_t)kvh * a.skh;
   const int64_t voff_h = (int64_t)kvh * a.svh;
-  const int32_t* bt_row = a.bt + (int64_t)b * a.sbb;
 
   for (int j = wave; j < nblk; j += nw) {
     const int t0 = t_begin + j * kBlockTokens;
     const _Float16* krow[4];
     const _Float16* vrow[4];
     if constexpr (UNIFORM) {
-      const int page = t0 / a.ps;
-      const int phys = clamp_page(load_uniform_i32(bt_row + (int64_t)page * a.sbp), a.num_pages);
+      const int page = page_of(a, t0);
+      const int phys = clamp_page(load_uniform_i32(bt_row + (int64_t)page * ids_stride), a.num_pages);
       const int slot0 = t0 - page * a.ps;
       const _Float16* kbase = a.k + (int64_t)phys * a.skp + koff_h + (int64_t)slot0 * a.sks;
       const _Float16* vbase = a.v + (int64_t)phys * a.svp + voff_h + (int64_t)slot0 * a.svs;
@@ -509,8 +532,8 @@ __device__ __forceinline__ void wave_loop_valu(const Phase1Args& a, int b, int k
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tv = min(t0 + 4 * g + i, t_end - 1);
-        const int page = tv / a.ps;
-        const int phys = clamp_page(bt_row[(int64_t)page * a.sbp], a.num_pages);
+        const int page = page_of(a, tv);
+        const int phys = clamp_page(bt_row[(int64_t)page * ids_stride], a.num_pages);
         const int slot = tv - page * a.ps;
         krow[i] = a.k + (int64_t)phys * a.skp + koff_h + (int64_t)slot * a.sks;
         vrow[i] = a.v + (int64_t)phys * a.svp + voff_h + (int64_t)slot * a.svs;
@@ -582,11 +605,299 @@ __device__ __forceinline__ void wave_loop_valu(const Phase1Args& a, int b, int k
     }
     if (g == 0) {
       if (r16 == 0) sm_ml[wave * 16 + r] = make_float2(M, l);
-      float* dst = sm_o + (wave * gqa + r) * D + r16 * DT;
+      float* dst = sm_o + (wave * gqa + r) * wave_row_floats<D>() + r16 * DT;
 #pragma unroll
       for (int e = 0; e < DT; ++e) dst[e] = acc[r][e];
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Work items.  Workgroup g of the grid (g = blockIdx.x + S*(blockIdx.y +
+// Hkv*blockIdx.z)) processes one item: a page range of one (sequence, kv
+// head) unit, and writes its partial to slot g of the workspace.  The items
+// of a unit occupy the consecutive slots [slot0, slot0 + nsplit).
+//  * Static items (an explicit split count, or every sequence at full
+//    capacity): item g is split blockIdx.x of unit (blockIdx.z, blockIdx.y),
+//    pages [s*pps, (s+1)*pps).
+//  * Planned items (heuristic split count, batch <= kPlanMaxBatch): every
+//    workgroup reads all sequence lengths and computes the same plan - the
+//    smallest chunk of c pages (c >= min_chunk) such that the units need at
+//    most G items, each unit cut into ceil(pages/c) chunks (an empty unit
+//    keeps one item, which writes its zero rows) - then takes item g in
+//    (sequence, kv head, chunk) order.  Ragged batches thus spread their
+//    pages evenly over the grid instead of leaving the splits of short
+//    sequences empty.
+// ---------------------------------------------------------------------------
+struct WorkItem {
+  int b, kvh;
+  int p_begin, p_end;  // logical pages [p_begin, p_end) of sequence b
+  int L;               // tokens of sequence b
+  int nsplit;          // items of the unit; 0: the unit is empty (write zeros)
+  int slot0;           // workspace slot of the unit's first item
+  int col_max;         // last page-id column that may be read speculatively
+  int valid;           // 0: no item for this workgroup
+  const int32_t* ids_row;
+  int64_t ids_stride;
+};
+
+// Wave-wide integer reductions: DPP within each 16-lane row, then the four
+// row results combined through readlane (wave-uniform result).
+__device__ __forceinline__ int row16_sum_i32(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  x += __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  x += __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);  // row_mirror
+  return x;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int x) {
+  x = row16_sum_i32(x);
+  return __builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16) + __builtin_amdgcn_readlane(x, 32) +
+         __builtin_amdgcn_readlane(x, 48);
+}
+
+__device__ __forceinline__ int wave_max_i32(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false));
+  return max(max(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+             max(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
+// Inclusive prefix sum over the 64 lanes: row_shr steps (bound_ctrl shifts
+// in zeros) scan each 16-lane row, then each row adds the totals of the rows
+// before it.
+__device__ __forceinline__ int wave_incl_scan_i32(int x, int lane) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(x, 15);
+  const int r1 = __builtin_amdgcn_readlane(x, 31);
+  const int r2 = __builtin_amdgcn_readlane(x, 47);
+  const int row = lane >> 4;
+  return x + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
+
+// CSR row of sequence b: first page-id offset, page count and tokens.  The
+// offsets are clamped into indices[0, max_pages) (max_pages holds the
+// length of `indices` in CSR mode), so a malformed indptr cannot make the
+// kernel read outside the array; last_page_len is clamped to the page.
+__device__ __forceinline__ void csr_row(const Phase1Args& a, int b, int* row, int* pages, int* len) {
+  const int r0 = min(max(a.indptr[b], 0), a.max_pages);
+  const int r1 = min(max(a.indptr[b + 1], r0), a.max_pages);
+  *row = r0;
+  *pages = r1 - r0;
+  *len = *pages > 0 ? (*pages - 1) * a.ps + min(max(a.lpl[b], 1), a.ps) : 0;
+}
+
+// Sequence table spread over the wave: lane l holds sequences l + 64k,
+// k < NK (NK = 1 for batches up to 64, else 4).
+template <int NK>
+struct SeqTable {
+  int len[NK];    // tokens (0 past the batch)
+  int pages[NK];  // pages in use
+  int row[NK];    // CSR: offset of the sequence's page ids in `indices`
+};
+
+// All loads are issued before any is used (one memory round trip); a lane
+// past the batch re-reads the last sequence's entries and discards them, so
+// no branch separates the loads.
+template <int NK>
+__device__ __forceinline__ SeqTable<NK> load_seq_table(const Phase1Args& a, int lane) {
+  SeqTable<NK> t;
+  int r0[NK], r1[NK], r2[NK];
+  if (a.csr) {
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      const int b = min(lane + 64 * k, a.batch - 1);
+      r0[k] = a.indptr[b];
+      r1[k] = a.indptr[b + 1];
+      r2[k] = a.lpl[b];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      r0[k] = a.sl[(int64_t)min(lane + 64 * k, a.batch - 1) * a.ssl];
+      r1[k] = r2[k] = 0;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const bool in = lane + 64 * k < a.batch;
+    int len, pages, row = 0;
+    if (a.csr) {
+      row = min(max(r0[k], 0), a.max_pages);
+      pages = min(max(r1[k], row), a.max_pages) - row;
+      len = pages > 0 ? (pages - 1) * a.ps + min(max(r2[k], 1), a.ps) : 0;
+    } else {
+      len = max(r0[k], 0);
+      pages = min(pages_for(a, len), a.max_pages);
+    }
+    t.len[k] = in ? len : 0;
+    t.pages[k] = in ? pages : 0;
+    t.row[k] = in ? row : 0;
+  }
+  return t;
+}
+
+// Value of lane (b % 64) of register k = b / 64 (b wave-uniform).
+template <int NK>
+__device__ __forceinline__ int seq_lane_value(const int (&v)[NK], int b) {
+  const int l = b & 63;
+  int x = __builtin_amdgcn_readlane(v[0], l);
+#pragma unroll
+  for (int k = 1; k < NK; ++k)
+    if ((b >> 6) == k) x = __builtin_amdgcn_readlane(v[k], l);
+  return x;
+}
+
+// ceil(p / c) for 0 <= p, c < 2^23: a float estimate corrected with exact
+// 24-bit products (the estimate is within one of the quotient).
+__device__ __forceinline__ int ceil_div_u23(int p, int c, float rc) {
+  int n = (int)__builtin_ceilf((float)p * rc);
+  n += (int)__umul24(n, c) < p ? 1 : 0;
+  n -= (n > 0 && (int)__umul24(n - 1, c) >= p) ? 1 : 0;
+  return n;
+}
+
+// Items per sequence with chunks of c pages (an empty sequence keeps one).
+__device__ __forceinline__ int items_for(int pages, int c, float rc) { return max(ceil_div_u23(pages, c, rc), 1); }
+
+// Items the units need for each of J chunk sizes (wave-uniform totals).  The
+// J evaluations are independent, so their latencies overlap.
+template <int NK, int J>
+__device__ __forceinline__ void plan_counts(const Phase1Args& a, const SeqTable<NK>& t, const int (&c)[J],
+                                            int (&n)[J], int lane) {
+  float rc[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    rc[j] = 1.0f / (float)c[j];
+    n[j] = 0;
+  }
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    const bool in = lane + 64 * k < a.batch;
+#pragma unroll
+    for (int j = 0; j < J; ++j) n[j] += in ? items_for(t.pages[k], c[j], rc[j]) : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) n[j] = row16_sum_i32(n[j]);
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    n[j] = (__builtin_amdgcn_readlane(n[j], 0) + __builtin_amdgcn_readlane(n[j], 16) +
+            __builtin_amdgcn_readlane(n[j], 32) + __builtin_amdgcn_readlane(n[j], 48)) *
+           a.hkv;
+}
+
+template <int NK>
+__device__ WorkItem plan_item(const Phase1Args& a, const SeqTable<NK>& t, int g, int G, int lane) {
+  WorkItem w;
+  int tot = 0, pmax = 0;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    tot += t.pages[k];
+    pmax = max(pmax, t.pages[k]);
+  }
+  tot = wave_sum_i32(tot);
+  pmax = max(wave_max_i32(pmax), 1);
+  // Chunk size: the smallest c >= c_lo whose item count fits the grid would
+  // be ideal, but every probe costs a pass over the table, so at most two
+  // are made.  c_lo = ceil(unit pages / G) (fits when the lengths divide
+  // evenly); then c_est, which assumes each non-empty unit rounds up by half
+  // a chunk; failing that c_hi = ceil(unit pages / (G - units)), which
+  // always fits since sum(ceil(p / c)) <= unit pages / c + units (and so
+  // does pmax: one item per unit, G >= units).
+  const int units = a.batch * a.hkv;
+  const int64_t unit_pages = (int64_t)tot * a.hkv;
+  int c = min(max(max(a.min_chunk, (int)((unit_pages + G - 1) / G)), 1), pmax);
+  int n1[1], c1[1] = {c};
+  plan_counts<NK, 1>(a, t, c1, n1, lane);
+  if (n1[0] > G) {
+    int c_hi = pmax;
+    if (G > units) c_hi = min(c_hi, (int)((unit_pages + (G - units) - 1) / (G - units)));
+    const int half = G - units / 2;
+    int c_est = half > 0 ? (int)((unit_pages + half - 1) / half) : c_hi;
+    c_est = max(c + 1, min(c_est, c_hi));
+    c1[0] = c_est;
+    plan_counts<NK, 1>(a, t, c1, n1, lane);
+    c = n1[0] <= G ? c_est : max(c_hi, c_est);
+  }
+  // Locate item g: units in (sequence, kv head) order, n_b items each.
+  w.valid = 0;
+  int carry = 0;
+  const float rc = 1.0f / (float)c;
+#pragma unroll
+  for (int k = 0; k < NK; ++k) {
+    if (64 * k >= a.batch) break;
+    const int b = lane + 64 * k;
+    const int nb = b < a.batch ? items_for(t.pages[k], c, rc) : 0;
+    const int x = nb * a.hkv;
+    const int incl = wave_incl_scan_i32(x, lane) + carry;
+    const int excl = incl - x;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(b < a.batch && excl <= g && g < incl);
+    if (hit != 0) {
+      const int l = (int)__builtin_ctzll(hit);
+      const int first = __builtin_amdgcn_readlane(excl, l);
+      const int n = __builtin_amdgcn_readlane(nb, l);
+      const int pages = __builtin_amdgcn_readlane(t.pages[k], l);
+      const int r = g - first;
+      w.b = 64 * k + l;
+      w.kvh = r / n;
+      const int chunk = r - w.kvh * n;
+      w.p_begin = chunk * c;
+      w.p_end = min(w.p_begin + c, pages);
+      w.L = __builtin_amdgcn_readlane(t.len[k], l);
+      w.nsplit = pages > 0 ? n : 0;
+      w.slot0 = first + w.kvh * n;
+      w.col_max = pages - 1;
+      w.ids_row = a.csr ? a.bt + __builtin_amdgcn_readlane(t.row[k], l) : a.bt + (int64_t)w.b * a.sbb;
+      w.valid = 1;
+      break;
+    }
+    carry = __builtin_amdgcn_readlane(incl, 63);
+  }
+  w.ids_stride = a.csr ? 1 : a.sbp;
+  return w;
+}
+
+// The static item of workgroup (s, kvh, b) given the sequence's length and
+// page count.
+__device__ __forceinline__ WorkItem static_item(const Phase1Args& a, int s, int kvh, int b, int L, int pages,
+                                                const int32_t* ids_row, int64_t ids_stride) {
+  WorkItem w;
+  w.b = b;
+  w.kvh = kvh;
+  w.L = L;
+  w.p_begin = s * a.pps;
+  w.p_end = min(w.p_begin + a.pps, pages);
+  w.nsplit = (pages + a.pps - 1) / a.pps;
+  w.slot0 = (b * a.hkv + kvh) * a.num_splits;
+  w.col_max = a.csr ? pages - 1 : a.max_pages - 1;
+  // Splits past the sequence's last page do nothing, except split 0 of an
+  // empty sequence, which writes its zero rows.
+  w.valid = s < w.nsplit || s == 0;
+  w.ids_row = ids_row;
+  w.ids_stride = ids_stride;
+  return w;
+}
+
+// Planned mode: read every sequence length; with every sequence at full
+// capacity the static split is already even, otherwise plan the items.
+template <int NK>
+__device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int g, int G, const int32_t* static_row,
+                                                 int lane) {
+  const SeqTable<NK> t = load_seq_table<NK>(a, lane);
+  bool full = !a.csr;
+#pragma unroll
+  for (int k = 0; k < NK; ++k)
+    if (lane + 64 * k < a.batch && t.pages[k] != a.max_pages) full = false;
+  if (__builtin_amdgcn_ballot_w64(!full) == 0)
+    return static_item(a, s, blockIdx.y, blockIdx.z, seq_lane_value<NK>(t.len, blockIdx.z), a.max_pages,
+                       static_row, a.sbp);
+  return plan_item<NK>(a, t, g, G, lane);
 }
 
 // Minimum waves per SIMD each phase-1 instantiation is compiled for (it
@@ -602,44 +913,71 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(phase1_wave
 void pad_phase1_kernel(const Phase1Args a) {
   extern __shared__ float4 smem_f4[];
   float2* sm_ml = reinterpret_cast<float2*>(smem_f4);  // [nw][16]
-  const int nw = blockDim.x >> 6;
-  float* sm_o = reinterpret_cast<float*>(smem_f4) + nw * 32;  // [nw][gqa][D]
+  const int nw = a.nw;
+  float* sm_o = reinterpret_cast<float*>(smem_f4) + nw * 32;  // [nw][gqa][D + 4]
   // [nw] K staging tiles (MFMA engine), after the wave states.
-  char* k_stage_all = reinterpret_cast<char*>(sm_o + nw * a.gqa * D);
+  char* k_stage_all = reinterpret_cast<char*>(sm_o + nw * a.gqa * wave_row_floats<D>());
 
   const int s = blockIdx.x;
-  const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = blockIdx.x + a.num_splits * (blockIdx.y + a.hkv * blockIdx.z);
+  const int G = a.num_splits * a.hkv * a.batch;
 
-  WavePrologue<D> pr;
-  if constexpr (ENGINE == 0) pr = wave_prologue<D, UNIFORM>(a, b, kvh, s, wave, lane);
-  const int L = max(a.sl[(int64_t)b * a.ssl], 0);
-  const int npages = min((L + a.ps - 1) / a.ps, a.max_pages);
-  const int nsplit = (npages + a.pps - 1) / a.pps;  // non-empty splits of this sequence
+  // Dense page table: read the first page id of this workgroup's static
+  // split before the sequence lengths arrive; it stays valid whenever the
+  // item turns out to be the static one.
+  const int32_t* static_row = a.bt + (int64_t)blockIdx.z * a.sbb;
+  int phys_first = 0;
+  if constexpr (ENGINE == 0 && UNIFORM) {
+    if (!a.csr) phys_first = first_page_id(a, static_row, a.sbp, a.max_pages - 1, s * a.pps, wave);
+  }
+  // Read unconditionally (any valid word when unused) after the page id, so
+  // both reads share one round trip.
+  const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)blockIdx.z * a.ssl);
+  WorkItem it;
+  if (a.balance) {
+    if (a.batch <= 64)
+      it = resolve_item<1>(a, s, g, G, static_row, lane);
+    else
+      it = resolve_item<4>(a, s, g, G, static_row, lane);
+  } else if (a.csr) {
+    const int b = blockIdx.z;
+    int row, pages, L;
+    csr_row(a, b, &row, &pages, &L);
+    it = static_item(a, s, blockIdx.y, b, L, pages, a.bt + row, 1);
+  } else {
+    const int L = max(static_len, 0);
+    it = static_item(a, s, blockIdx.y, blockIdx.z, L, min(pages_for(a, L), a.max_pages), static_row, a.sbp);
+  }
+  if (!it.valid) return;
+  const int b = it.b;
+  const int kvh = it.kvh;
+  const int nsplit = it.nsplit;
   const int gqa = a.gqa;
   const int total4 = gqa * (D / 4);
   _Float16* out_bh = a.out + (int64_t)b * a.sob + (int64_t)(kvh * gqa) * a.soh;
-  if (s >= nsplit) {  // empty split
-    if (s == 0) {     // seq_len == 0: the output rows are zeros
-      for (int e = threadIdx.x; e < total4; e += blockDim.x) {
-        const int row = e / (D / 4);
-        *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + (e - row * (D / 4)) * 4) = (h4_t)0;
-      }
+  if (nsplit == 0) {  // seq_len == 0: the output rows are zeros
+    for (int e = threadIdx.x; e < total4; e += nw * 64) {
+      const int row = e / (D / 4);
+      *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + (e - row * (D / 4)) * 4) = (h4_t)0;
     }
     return;
   }
-  const int p0 = s * a.pps;
-  const int t_begin = p0 * a.ps;
-  const int t_end = min(min(p0 + a.pps, npages) * a.ps, L);
+  if constexpr (ENGINE == 0 && UNIFORM) {
+    if (a.csr || b != (int)blockIdx.z || it.p_begin != s * a.pps)
+      phys_first = first_page_id(a, it.ids_row, it.ids_stride, it.col_max, it.p_begin, wave);
+  }
+  const int t_begin = it.p_begin * a.ps;
+  const int t_end = min(it.p_end * a.ps, it.L);
   const int nblk = (t_end - t_begin + kBlockTokens - 1) / kBlockTokens;
 
   if constexpr (ENGINE == 0) {
-    wave_loop_mfma<D, UNIFORM>(a, pr, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o,
-                               k_stage_all + wave * k_stage_bytes<D>());
+    wave_loop_mfma<D, UNIFORM>(a, phys_first, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw,
+                               lane, sm_ml, sm_o, k_stage_all + wave * k_stage_bytes<D>());
   } else {
-    wave_loop_valu<D, UNIFORM, GQA_T>(a, b, kvh, t_begin, t_end, nblk, wave, nw, lane, sm_ml, sm_o);
+    wave_loop_valu<D, UNIFORM, GQA_T>(a, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw, lane,
+                                      sm_ml, sm_o);
   }
   __syncthreads();
 
@@ -647,24 +985,39 @@ void pad_phase1_kernel(const Phase1Args a) {
   // single split the result is final; otherwise it is this split's partial.
   // Partials are stored and later loaded with device-scope (SC1) buffer
   // accesses, which are coherent across the XCDs' L2 caches on their own, so
-  // publishing a partial needs no cache writeback.  Each (sequence, kv head)
-  // owns a contiguous partial region, addressed with 32-bit byte offsets.
-  const int64_t seq_row0 = ((int64_t)b * a.hkv + kvh) * a.num_splits * gqa;
-  const uint32_t region_rows = (uint32_t)(a.num_splits * gqa);
+  // publishing a partial needs no cache writeback.  The items of a (sequence,
+  // kv head) own consecutive slots, addressed with 32-bit byte offsets.
+  const int64_t seq_row0 = (int64_t)it.slot0 * gqa;
+  const uint32_t region_rows = (uint32_t)(nsplit * gqa);
   const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o_part + seq_row0 * D, region_rows * D * 4u);
   const __amdgpu_buffer_rsrc_t ml_rsrc = make_rsrc(a.ml_part + seq_row0, region_rows * 8u);
-  for (int e = threadIdx.x; e < total4; e += blockDim.x) {
+  const int my_split = g - it.slot0;
+  for (int e = threadIdx.x; e < total4; e += nw * 64) {
     const int row = e / (D / 4);
     const int col = (e - row * (D / 4)) * 4;
+    // Unrolled over the largest wave count, so all LDS reads issue together.
+    float2 ml[kMaxWaves];
+    f4_t ow[kMaxWaves];
+#pragma unroll
+    for (int w = 0; w < kMaxWaves; ++w) {
+      if (w < nw) {
+        ml[w] = sm_ml[w * 16 + row];
+        ow[w] = *reinterpret_cast<const f4_t*>(sm_o + (w * gqa + row) * wave_row_floats<D>() + col);
+      }
+    }
     float M = kNegInf;
-    for (int w = 0; w < nw; ++w) M = fmaxf(M, sm_ml[w * 16 + row].x);
+#pragma unroll
+    for (int w = 0; w < kMaxWaves; ++w)
+      if (w < nw) M = fmaxf(M, ml[w].x);
     f4_t acc = (f4_t)0.f;
     float Ls = 0.f;
-    for (int w = 0; w < nw; ++w) {
-      const float2 ml = sm_ml[w * 16 + row];
-      const float c = (ml.x == kNegInf) ? 0.f : exp2_fast(ml.x - M);
-      Ls += c * ml.y;
-      acc += c * *reinterpret_cast<const f4_t*>(sm_o + (w * gqa + row) * D + col);
+#pragma unroll
+    for (int w = 0; w < kMaxWaves; ++w) {
+      if (w < nw) {
+        const float c = (ml[w].x == kNegInf) ? 0.f : exp2_fast(ml[w].x - M);
+        Ls += c * ml[w].y;
+        acc += c * ow[w];
+      }
     }
     if (nsplit == 1) {
       const float inv = 1.f / Ls;  // Ls >= 1: the max token contributes 2^0
@@ -673,7 +1026,7 @@ void pad_phase1_kernel(const Phase1Args a) {
       for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
       *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + col) = hv;
     } else {
-      const uint32_t r = (uint32_t)(s * gqa + row);
+      const uint32_t r = (uint32_t)(my_split * gqa + row);
       store_device(o_rsrc, (r * D + col) * 4u, acc);
       if (col == 0) store_device(ml_rsrc, r * 8u, make_float2(M, Ls));
     }
@@ -695,7 +1048,7 @@ void pad_phase1_kernel(const Phase1Args a) {
   }
   __syncthreads();
   if (!s_last) return;
-  for (int e = threadIdx.x; e < total4; e += blockDim.x) {
+  for (int e = threadIdx.x; e < total4; e += nw * 64) {
     const int row = e / (D / 4);
     const int col = (e - row * (D / 4)) * 4;
     float m = kNegInf, l = 0.f;
@@ -734,7 +1087,7 @@ static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 static bool valu_supported(int d, int gqa) { return (d == 64 || d == 128) && gqa <= 8; }
 
 static int merge_wave_cap(int gqa, int d) {
-  const int per_wave = 16 * 8 + gqa * d * 4;
+  const int per_wave = 16 * 8 + gqa * (d + 4) * 4;
   int cap = kMergeLdsBudget / per_wave;
   if (cap > kMaxWaves) cap = kMaxWaves;
   if (cap < 1) cap = 1;
@@ -755,9 +1108,10 @@ static int validate_dims(const pad_decode_dims* d) {
 }
 
 // Workspace layout (from the first 256-byte boundary of the buffer); the
-// workspace holds no state between launches:
-//   o_part   fp32  [B, Hkv, S, gqa, D] unnormalised split outputs
-//   ml_part  fp32x2 [B, Hkv, S, gqa]   (m in base-2 units, l)
+// workspace holds no state between launches.  One slot per workgroup of the
+// (S, Hkv, B) grid, G = B * Hkv * S slots:
+//   o_part   fp32  [G, gqa, D] unnormalised split outputs
+//   ml_part  fp32x2 [G, gqa]   (m in base-2 units, l)
 // Returns the bytes needed (including 256 bytes of alignment slack) and,
 // when `ws` is given, the region pointers.
 static size_t workspace_layout(const pad_decode_dims* d, int S, void* ws, float** o_part, float2** ml_part) {
@@ -803,7 +1157,6 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     // are then equal) with at least kMinBlocks 16-token blocks per split, so
     // each workgroup's fixed costs (q load, wave merge, partial publish)
     // stay small against its streaming.
-    constexpr int64_t kMinBlocks = 16;
     const int64_t max_groups = latency_bound ? num_cus / 2 : num_cus;
     int64_t s_want = 1;
     while (s_want * 2 * units <= max_groups) s_want *= 2;
@@ -883,10 +1236,13 @@ static hipError_t dispatch_phase1(const Phase1Args& a, dim3 grid, int nw, size_t
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Dense page table: bt = block_table, sl = seq_lens, indptr = lpl = NULL.
+// CSR: bt = indices, indptr / lpl given, sl unused (dims->max_pages is the
+// number of entries in indices).
 static int launch_impl(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
-                       void* out, void* ws, size_t ws_bytes, int32_t* counters, int64_t num_counters,
-                       const pad_decode_dims* d, float scale, int num_splits, int engine, void* const* events,
-                       void* stream) {
+                       const int32_t* indptr, const int32_t* lpl, void* out, void* ws, size_t ws_bytes,
+                       int32_t* counters, int64_t num_counters, const pad_decode_dims* d, float scale,
+                       int num_splits, int engine, void* const* events, void* stream) {
   if (engine != 0 && engine != 1) return PAD_ERR_INVALID_SHAPE;
   int cus = 0;
   int st = device_cus(&cus);
@@ -897,7 +1253,9 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   const int gqa = d->num_q_heads / d->num_kv_heads;
   if (engine == 1 && !valu_supported(d->head_dim, gqa)) return PAD_ERR_UNSUPPORTED_GQA;
   if (d->batch == 0) return PAD_OK;
-  if (!q || !k || !v || !bt || !sl || !out) return PAD_ERR_NULL_POINTER;
+  const bool csr = indptr != nullptr || lpl != nullptr;
+  if (!q || !k || !v || !out) return PAD_ERR_NULL_POINTER;
+  if (csr ? (!indptr || !lpl || (!bt && d->max_pages > 0)) : (!bt || !sl)) return PAD_ERR_NULL_POINTER;
   // 16-byte rows: every K/V/q/out row start must be 16-byte aligned.
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return PAD_ERR_ALIGNMENT;
   if ((d->q_stride[0] | d->q_stride[1]) % 8 || (d->out_stride[0] | d->out_stride[1]) % 8 ||
@@ -919,6 +1277,8 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.v = static_cast<const _Float16*>(v);
   a.bt = bt;
   a.sl = sl;
+  a.indptr = indptr;
+  a.lpl = lpl;
   a.out = static_cast<_Float16*>(out);
   a.o_part = o_part;
   a.ml_part = ml_part;
@@ -931,8 +1291,8 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.svp = d->v_stride[0];
   a.svs = d->v_stride[1];
   a.svh = d->v_stride[2];
-  a.sbb = d->bt_stride[0];
-  a.sbp = d->bt_stride[1];
+  a.sbb = csr ? 0 : d->bt_stride[0];
+  a.sbp = csr ? 1 : d->bt_stride[1];
   a.ssl = d->sl_stride;
   a.sob = d->out_stride[0];
   a.soh = d->out_stride[1];
@@ -943,13 +1303,24 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.num_splits = S;
   a.hkv = d->num_kv_heads;
   a.max_pages = d->max_pages;
+  a.batch = d->batch;
+  a.csr = csr ? 1 : 0;
+  // The in-kernel planner evens out ragged batches; an explicit split count
+  // keeps its meaning (that many page-aligned splits per sequence).
+  a.balance = (num_splits == 0 && !plan.single_pass && d->batch <= kPlanMaxBatch && d->max_pages < (1 << 23)) ? 1 : 0;
+  a.min_chunk = ceil_div(kMinBlocks * kBlockTokens, d->page_size);
+  a.ps_shift = -1;
+  for (int sh = 0; sh < 31; ++sh)
+    if ((1 << sh) == d->page_size) a.ps_shift = sh;
   a.scale_log2 = scale * kLog2e;
+  a.nw = plan.waves_per_group;
 
   const int nw = plan.waves_per_group;
-  // Dynamic LDS: wave (m, l) [nw][16], wave O [nw][gqa][D], and for the MFMA
+  // Dynamic LDS: wave (m, l) [nw][16], wave O [nw][gqa][D + 4], and for the MFMA
   // engine one padded 16-row K staging tile per wave.
   const size_t k_stage = engine == 0 ? (size_t)nw * 16 * (d->head_dim * 2 + 16) : 0;
-  const size_t lds = (size_t)nw * 16 * sizeof(float2) + (size_t)nw * gqa * d->head_dim * sizeof(float) + k_stage;
+  const size_t lds =
+      (size_t)nw * 16 * sizeof(float2) + (size_t)nw * gqa * (d->head_dim + 4) * sizeof(float) + k_stage;
   const dim3 grid1(S, d->num_kv_heads, d->batch);
 
   if (events && events[0] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[0]), hs) != hipSuccess)
@@ -1001,16 +1372,25 @@ int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache, c
                       const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
                       int32_t* counters, int64_t num_counters, const pad_decode_dims* dims, float scale,
                       int num_splits, void* stream) {
-  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, out, workspace, workspace_bytes, counters,
-                          num_counters, dims, scale, num_splits, 0, nullptr, stream);
+  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, nullptr, nullptr, out, workspace,
+                          workspace_bytes, counters, num_counters, dims, scale, num_splits, 0, nullptr, stream);
+}
+
+int pad_decode_launch_csr(const void* q, const void* k_cache, const void* v_cache, const int32_t* indices,
+                          const int32_t* indptr, const int32_t* last_page_len, void* out, void* workspace,
+                          size_t workspace_bytes, int32_t* counters, int64_t num_counters,
+                          const pad_decode_dims* dims, float scale, int num_splits, int engine, void* stream) {
+  if (!indptr || !last_page_len) return PAD_ERR_NULL_POINTER;
+  return pad::launch_impl(q, k_cache, v_cache, indices, nullptr, indptr, last_page_len, out, workspace,
+                          workspace_bytes, counters, num_counters, dims, scale, num_splits, engine, nullptr, stream);
 }
 
 int pad_decode_launch_ex(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                          const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
                          int32_t* counters, int64_t num_counters, const pad_decode_dims* dims, float scale,
                          int num_splits, int engine, void* const* events, void* stream) {
-  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, out, workspace, workspace_bytes, counters,
-                          num_counters, dims, scale, num_splits, engine, events, stream);
+  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, nullptr, nullptr, out, workspace,
+                          workspace_bytes, counters, num_counters, dims, scale, num_splits, engine, events, stream);
 }
 
 int pad_decode_counters_init(int32_t* counters, int64_t num_counters, void* stream) {

@@ -5,7 +5,8 @@
 // (cuda/kernel_v4_split_k.cu:205-268).  This file holds no kernels: it reads
 // shapes, strides and data pointers from the tensors, allocates the output
 // from PyTorch's caching allocator, and calls
-// pad_decode_launch_ex() on PyTorch's current HIP stream of q's device, with
+// pad_decode_launch_ex() (or pad_decode_launch_csr()) on PyTorch's current HIP
+// stream of q's device, with
 // persistent split scratch (workspace + arrival counters) per (device,
 // stream).
 // Argument errors surface as RuntimeError (the reference used TORCH_CHECK,
@@ -144,6 +145,65 @@ torch::Tensor forward_events(torch::Tensor q, torch::Tensor k_cache, torch::Tens
   return forward_impl(q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, engine, evs);
 }
 
+// Decode with a CSR page index: the page ids of sequence b are
+// indices[indptr[b] : indptr[b+1]] and its last page holds last_page_len[b]
+// tokens (the (indptr, indices, last_page_len) triple the reference's
+// FlashInfer adapter builds, src/flashinfer_adapter.py:40-65).
+torch::Tensor forward_csr(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor indptr,
+                          torch::Tensor indices, torch::Tensor last_page_len, double scale, int64_t num_splits,
+                          int64_t engine) {
+  TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && indptr.is_cuda() && indices.is_cuda() &&
+                  last_page_len.is_cuda(),
+              "pa_decode: all tensors must be on the GPU");
+  TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() && q.device() == indptr.device() &&
+                  q.device() == indices.device() && q.device() == last_page_len.device(),
+              "pa_decode: all tensors must be on the same device");
+  TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
+                  v_cache.scalar_type() == at::kHalf,
+              "pa_decode: q, k_cache and v_cache must be float16");
+  TORCH_CHECK(indptr.scalar_type() == at::kInt && indices.scalar_type() == at::kInt &&
+                  last_page_len.scalar_type() == at::kInt,
+              "pa_decode: indptr, indices and last_page_len must be int32");
+  TORCH_CHECK(q.dim() == 3, "pa_decode: q must be [batch, num_q_heads, head_dim]");
+  TORCH_CHECK(k_cache.dim() == 4, "pa_decode: k_cache must be [num_pages, page_size, num_kv_heads, head_dim]");
+  TORCH_CHECK(v_cache.sizes() == k_cache.sizes(), "pa_decode: v_cache shape must match k_cache");
+  TORCH_CHECK(indptr.dim() == 1 && indptr.size(0) == q.size(0) + 1, "pa_decode: indptr must be [batch + 1]");
+  TORCH_CHECK(last_page_len.dim() == 1 && last_page_len.size(0) == q.size(0),
+              "pa_decode: last_page_len must be [batch]");
+  TORCH_CHECK(indices.dim() == 1 && indices.is_contiguous() && indptr.is_contiguous() &&
+                  last_page_len.is_contiguous(),
+              "pa_decode: indptr, indices and last_page_len must be contiguous 1-D tensors");
+  TORCH_CHECK(indices.size(0) <= INT32_MAX, "pa_decode: too many page ids");
+  TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
+
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+  pad_decode_dims d;
+  fill_dims(q, k_cache, v_cache, indices.view({1, -1}), last_page_len, out, &d);
+  d.max_pages = static_cast<int32_t>(indices.size(0));
+  d.bt_stride[0] = 0;
+  d.bt_stride[1] = 1;
+
+  const int cus = cached_cus(q.get_device());
+  pad_decode_plan_t plan;
+  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cus, &plan);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  void* ws_ptr = nullptr;
+  int32_t* counters = nullptr;
+  if (!plan.single_pass) {
+    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
+    ws_ptr = sc.workspace.data_ptr();
+    counters = sc.counters.data_ptr<int32_t>();
+  }
+  st = pad_decode_launch_csr(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), indices.data_ptr<int32_t>(),
+                             indptr.data_ptr<int32_t>(), last_page_len.data_ptr<int32_t>(), out.data_ptr(), ws_ptr,
+                             plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
+                             static_cast<int>(num_splits), static_cast<int>(engine), stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return out;
+}
+
 // Same argument list as the reference's forward_v4 binding
 // (cuda/kernels.h:60-70): gqa_ratio, head_dim and page_size must agree with
 // the tensor shapes.
@@ -193,6 +253,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_events", &forward_events,
         "forward() recording three hipEvent_t handles: before phase 1, after phase 1, after phase 2");
   m.def("forward_v4", &forward_v4, "Paged-attention decode with the reference forward_v4 argument list");
+  m.def("forward_csr", &forward_csr,
+        "Paged-attention decode over a CSR page index (q, k_cache, v_cache, indptr, indices, last_page_len, "
+        "scale, num_splits, engine) -> out");
   m.def("plan", &plan, "Split plan for the given shapes (host only)");
   m.def("abi_version", &pad_decode_abi_version, "C ABI version of the linked libpa_decode.so");
 }

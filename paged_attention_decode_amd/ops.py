@@ -90,6 +90,74 @@ def paged_attention_decode(q, k_cache, v_cache, block_table, seq_lens, num_split
 paged_attention_decode_cuda_v4 = paged_attention_decode
 
 
+def paged_kv_indices(block_table, seq_lens, page_size: int):
+    """Dense ``block_table [B, max_pages]`` + ``seq_lens [B]`` -> CSR ``(indptr, indices, last_page_len)``.
+
+    The conversion of the reference's FlashInfer adapter,
+    ``_paged_kv_indices`` (src/flashinfer_adapter.py:40-65): sequence b uses
+    its first ``ceil(seq_lens[b] / page_size)`` pages, ``indptr`` is the
+    running page count (int32, ``[B + 1]``), ``indices`` the used page ids in
+    order (int32) and ``last_page_len[b] = seq_lens[b] - (pages_b - 1) *
+    page_size`` (int32; in [1, page_size] for a non-empty sequence).  Done
+    with tensor ops on the tables' device; sizing ``indices`` reads the total
+    page count back to the host once.
+    """
+    assert block_table.dim() == 2 and seq_lens.dim() == 1 and block_table.shape[0] == seq_lens.shape[0], (
+        "block_table must be [batch, max_pages] and seq_lens [batch]"
+    )
+    assert page_size >= 1, "page_size must be >= 1"
+    device = block_table.device
+    lens = seq_lens.to(torch.int64)
+    pages = (lens + page_size - 1) // page_size
+    indptr = torch.zeros(seq_lens.shape[0] + 1, dtype=torch.int32, device=device)
+    indptr[1:] = torch.cumsum(pages, dim=0).to(torch.int32)
+    cols = torch.arange(block_table.shape[1], device=device)
+    used = cols.unsqueeze(0) < pages.unsqueeze(1)
+    indices = block_table[used].to(torch.int32)
+    last_page_len = (lens - (pages - 1) * page_size).to(torch.int32)
+    return indptr, indices, last_page_len
+
+
+def paged_attention_decode_csr(q, k_cache, v_cache, indptr, indices, last_page_len, num_splits=None, scale=None,
+                               engine: int = ENGINE_MFMA):
+    """Paged-attention decode over a CSR page index (no dense block table).
+
+    Sequence b's page ids are ``indices[indptr[b]:indptr[b+1]]`` and its last
+    page holds ``last_page_len[b]`` tokens - FlashInfer's paged-KV index, which
+    the reference builds in src/flashinfer_adapter.py:40-65 and hands to
+    ``BatchDecodeWithPagedKVCacheWrapper.plan/run`` (:100-112).  Same caches,
+    ``scale`` and ``num_splits`` as :func:`paged_attention_decode`; returns
+    fp16 shaped like q.  Index tensors may be int32 or int64 (cast to int32).
+    """
+    assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "paged_attention_decode requires GPU tensors"
+    assert indptr.is_cuda and indices.is_cuda and last_page_len.is_cuda, "CSR index tensors must be GPU tensors"
+    assert q.dtype == torch.float16 and k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16, (
+        "paged_attention_decode expects fp16 q/k_cache/v_cache"
+    )
+    assert q.dim() == 3 and k_cache.dim() == 4 and v_cache.shape == k_cache.shape, "bad q / cache shapes"
+    batch, num_q_heads, head_dim = q.shape
+    num_kv_heads = k_cache.shape[2]
+    assert k_cache.shape[3] == head_dim, "q head_dim must match the KV cache head_dim"
+    assert num_q_heads % num_kv_heads == 0, "num_q_heads must be divisible by num_kv_heads (GQA)"
+    assert num_q_heads // num_kv_heads <= MAX_GQA, f"GQA group larger than {MAX_GQA}"
+    assert head_dim in SUPPORTED_HEAD_DIMS, f"head_dim must be one of {SUPPORTED_HEAD_DIMS}"
+    assert indptr.dim() == 1 and indptr.shape[0] == batch + 1, "indptr must be [batch + 1]"
+    assert last_page_len.dim() == 1 and last_page_len.shape[0] == batch, "last_page_len must be [batch]"
+    assert indices.dim() == 1, "indices must be 1-D"
+    assert k_cache.stride(3) == 1 and v_cache.stride(3) == 1, "K/V caches need a contiguous head_dim"
+    if num_splits is None:
+        num_splits = 0
+    else:
+        num_splits = int(num_splits)
+        assert num_splits >= 1, "num_splits must be >= 1"
+    indptr = indptr.to(torch.int32).contiguous()
+    indices = indices.to(torch.int32).contiguous()
+    last_page_len = last_page_len.to(torch.int32).contiguous()
+    scale = float(scale) if scale is not None else 1.0 / math.sqrt(head_dim)
+    return ext().forward_csr(_aligned_q(q), k_cache, v_cache, indptr, indices, last_page_len, scale, num_splits,
+                             int(engine))
+
+
 def plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits=0, num_cus=0):
     """Split plan the native launcher would use (host only), as a dict."""
     return ext().plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits, num_cus)

@@ -51,7 +51,7 @@ def test_library_exports_every_declared_symbol():
     lib = _native.capi()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.pad_decode_abi_version() == 1
+    assert lib.pad_decode_abi_version() == 2
 
 
 def test_status_strings():
@@ -251,3 +251,47 @@ def test_launch_rejects_bad_arguments_without_launching():
     assert lib.pad_decode_launch_ex(q16.data_ptr(), k.data_ptr(), k.data_ptr(), bt.data_ptr(), sl.data_ptr(),
                                     q16.data_ptr(), None, 0, None, 0, ctypes.byref(dm16), 0.1, 1, 1, None, None) == 4
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("splits", [0, 3])
+def test_launch_csr_through_c_abi(splits):
+    """pad_decode_launch_csr with a caller-owned workspace, counters and stream."""
+    from oracle.csr import paged_kv_indices
+    from oracle.reference import decode_fp16_protocol
+
+    lib = _native.capi()
+    lens = [0, 5, 77, 400, 1000]
+    bt, n = shuffled_table(lens, 16, spare_pages=3, extra_cols=1, seed=5)
+    k, v = make_cache(n, 16, 2, 128, seed=5)
+    q = torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(5))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    expected = decode_fp16_protocol(q, k, v, bt, sl)
+    indptr, indices, last = (x.cuda() for x in paged_kv_indices(bt, sl, 16))
+    qd, kd, vd = q.half().cuda(), k.half().cuda(), v.half().cuda()
+    out = torch.empty_like(qd)
+    dm = _native.dims_for(qd, kd, vd, indices.view(1, -1), last, out)
+    dm.bt_stride[0], dm.bt_stride[1] = 0, 1
+    wsb = ctypes.c_size_t()
+    nc = ctypes.c_int64()
+    assert lib.pad_decode_workspace_bytes(ctypes.byref(dm), splits, 0, ctypes.byref(wsb)) == 0
+    assert lib.pad_decode_counters_needed(ctypes.byref(dm), splits, 0, ctypes.byref(nc)) == 0
+    ws = torch.empty(max(wsb.value, 1), dtype=torch.uint8, device="cuda")
+    counters = torch.zeros(max(nc.value, 1), dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+    for _ in range(2):
+        out.fill_(float("nan"))
+        ws.fill_(0x7F)
+        torch.cuda.synchronize()
+        st = lib.pad_decode_launch_csr(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), indices.data_ptr(),
+                                       indptr.data_ptr(), last.data_ptr(), out.data_ptr(), ws.data_ptr(), wsb.value,
+                                       counters.data_ptr(), counters.numel(), ctypes.byref(dm), 1.0 / 128 ** 0.5,
+                                       splits, 0, stream.cuda_stream)
+        assert st == 0, lib.pad_status_string(st)
+        stream.synchronize()
+        assert_parity(out, expected)
+        assert torch.all(counters == 0), counters
+    # Missing CSR arrays are rejected before any launch.
+    assert lib.pad_decode_launch_csr(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), indices.data_ptr(), None,
+                                     last.data_ptr(), out.data_ptr(), ws.data_ptr(), wsb.value, counters.data_ptr(),
+                                     counters.numel(), ctypes.byref(dm), 0.1, splits, 0, None) == 1
