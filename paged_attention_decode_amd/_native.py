@@ -7,6 +7,8 @@
   for every entry point of include/pa_decode.h, plus the ``PadDims`` /
   ``PadPlan`` structures that mirror ``pad_decode_dims`` /
   ``pad_decode_plan_t``.
+* ``probe()`` - ``libpa_probe.so``, the bandwidth probes used by
+  ``roofline.py`` (measurement tooling, not the decode path).
 
 Both raise ImportError with the build command when the library is missing;
 nothing here computes attention on the CPU.
@@ -125,6 +127,36 @@ def capi():
             fn.restype = restype
         _capi = lib
     return _capi
+
+
+PROBE_PATH = os.path.join(_PKG_DIR, "libpa_probe.so")
+PROBE_SIGNATURES = {
+    "pad_probe_stream_read": (
+        [_VP, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP, _VP],
+        ctypes.c_int,
+    ),
+    "pad_probe_paged_read": (
+        [_VP, _VP, _VP, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+         ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP, _VP],
+        ctypes.c_int,
+    ),
+}
+_probe = None
+
+
+def probe():
+    """ctypes handle to libpa_probe.so (bandwidth probes of the roofline report)."""
+    global _probe
+    if _probe is None:
+        if not os.path.exists(PROBE_PATH):
+            raise ImportError(f"paged_attention_decode_amd: {PROBE_PATH} is missing; {_BUILD_HINT}")
+        lib = ctypes.CDLL(PROBE_PATH)
+        for name, (argtypes, restype) in PROBE_SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        _probe = lib
+    return _probe
 
 
 def dims_for(q, k_cache, v_cache, block_table, seq_lens, out) -> PadDims:

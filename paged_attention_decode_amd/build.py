@@ -1,6 +1,6 @@
 """Build the native parts of the package in-tree.
 
-Two shared libraries, both written next to this file:
+Three shared libraries, all written next to this file:
 
 * ``libpa_decode.so`` - the C-ABI library (``include/pa_decode.h``): gfx950
   kernels plus ``extern "C"`` entry points, compiled by ``hipcc`` from
@@ -9,6 +9,8 @@ Two shared libraries, both written next to this file:
   (``csrc/pa_torch.cpp``), host-only C++ compiled by ``g++`` against
   PyTorch's headers and linked to ``libpa_decode.so`` through an
   ``$ORIGIN`` rpath.
+* ``libpa_probe.so`` - bandwidth probes for the roofline report
+  (``csrc/pa_probe.hip``, ``roofline.py``); not on the decode path.
 
 Usage: ``python -m paged_attention_decode_amd.build`` (or ``build()`` from
 ``__graft_entry__``).  Every call recompiles.
@@ -30,6 +32,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 CAPI_LIB = os.path.join(PKG_DIR, "libpa_decode.so")
+PROBE_LIB = os.path.join(PKG_DIR, "libpa_probe.so")
 EXT_NAME = "_pa_decode_ext"
 EXT_LIB = os.path.join(PKG_DIR, EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
 
@@ -65,6 +68,15 @@ def build_capi() -> str:
     _run([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", os.path.join(CSRC, "pa_decode.hip"), "-o", tmp])
     os.replace(tmp, CAPI_LIB)
     return CAPI_LIB
+
+
+def build_probe() -> str:
+    """libpa_probe.so: the bandwidth probes of the roofline report (roofline.py)."""
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    tmp = PROBE_LIB + ".tmp"
+    _run([hipcc, *HIP_FLAGS, os.path.join(CSRC, "pa_probe.hip"), "-o", tmp])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 def build_torch_ext() -> str:
@@ -111,7 +123,7 @@ def build_torch_ext() -> str:
 
 
 def build_all() -> list[str]:
-    return [build_capi(), build_torch_ext()]
+    return [build_capi(), build_torch_ext(), build_probe()]
 
 
 if __name__ == "__main__":

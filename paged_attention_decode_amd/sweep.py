@@ -1,0 +1,88 @@
+"""Split-count sweep: µs per decode call for each num_splits, against the heuristic.
+
+    python -m paged_attention_decode_amd.sweep [--config C2] [--batch 1] [--splits 1,2,4,...] [--json out.json]
+
+The MI355X counterpart of the reference's bench/bench_cuda_v4_num_splits.py
+(which swept num_splits 1..128 at batch 1 to choose its fixed default of 64,
+src/kernel_cuda_v4.py:16).  Same measuring discipline: every setting is timed
+in interleaved trials (each the best of ``--iters`` event-bracketed calls
+after a warm-up), and the median over ``--trials`` trials is reported, so
+clock and power-state drift hits all settings alike.  The heuristic's own
+choice (``num_splits=None``: the plan of csrc/pa_decode.hip, with in-kernel
+balancing of ragged batches) is timed as one more setting; the plan it picks
+is printed with it.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+
+import torch
+
+from . import paged_attention_decode, plan
+from . import workloads as wl
+
+
+def _best_of(fn, iters):
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = float("inf")
+    for _ in range(iters):
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        best = min(best, s.elapsed_time(e))
+    return best * 1e3  # us
+
+
+def sweep(name, batch, splits, trials=9, iters=30, warmup=10):
+    w = wl.make(name, batch=batch, seed=7)
+    settings = [None] + list(splits)
+    fns = {s: (lambda s=s: paged_attention_decode(*w.args(), num_splits=s)) for s in settings}
+    for s in settings:
+        for _ in range(warmup):
+            fns[s]()
+    torch.cuda.synchronize()
+    samples = {s: [] for s in settings}
+    for _ in range(trials):
+        for s in settings:
+            samples[s].append(_best_of(fns[s], iters))
+    shp = w.shape
+    chosen = plan(shp["batch"], shp["num_q_heads"], shp["num_kv_heads"], shp["head_dim"], shp["page_size"],
+                  shp["max_pages"], 0)
+    nbytes = wl.bytes_of(w)
+    rows = []
+    for s in settings:
+        us = statistics.median(samples[s])
+        rows.append({"num_splits": "heuristic" if s is None else s, "us_per_call": round(us, 2),
+                     "gbs": round(nbytes / us / 1e3, 1)})
+    return {"config": w.name, "algorithmic_bytes": nbytes, "heuristic_plan": chosen, "rows": rows}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--config", default="C2")
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--splits", default="1,2,4,8,16,32,64,128")
+    ap.add_argument("--trials", type=int, default=9)
+    ap.add_argument("--iters", type=int, default=30)
+    ap.add_argument("--json", default="")
+    a = ap.parse_args()
+    assert torch.cuda.is_available(), "the sweep needs a GPU"
+    res = sweep(a.config, a.batch, [int(x) for x in a.splits.split(",")], a.trials, a.iters)
+    p = res["heuristic_plan"]
+    print(f"{res['config']}: {res['algorithmic_bytes']} algorithmic bytes per call (warm inputs); heuristic plan: "
+          f"{p['num_splits']} splits x {p['waves_per_group']} waves, {p['pages_per_split']} pages per split")
+    best = min(res["rows"], key=lambda r: r["us_per_call"])
+    for r in res["rows"]:
+        mark = "  <- fastest" if r is best else ""
+        print(f"  num_splits={str(r['num_splits']):>9s}  {r['us_per_call']:8.2f} us  {r['gbs']:8.1f} GB/s{mark}")
+    if a.json:
+        with open(a.json, "w") as f:
+            json.dump(res, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()
