@@ -25,6 +25,13 @@ What one run measures (one GPU; ``--gpus`` above 1 exits with a message):
   of the reference's src/reference.py) timed on the host cores on the same
   headline inputs for a bounded sample (about --cpu-seconds of work), in the
   same GB/s unit.
+* ``roofline.measured_ceiling_gbs``: what a read-only kernel with the
+  decode's own access pattern (K and V tiles of the same pages, no
+  arithmetic; libpa_probe.so via roofline.ceilings) reaches on the same
+  rotated inputs - the practical ceiling for this page layout.
+* ``c3_ragged``: configuration C3 (batch 32, seq_lens uniform in
+  [1, 8192], page 32) through the drop-in (in-kernel planned splits) and
+  through the CSR page-index entry, cold throughput.
 """
 
 from __future__ import annotations
@@ -58,6 +65,8 @@ def _parse():
     p.add_argument("--num-splits", type=int, default=0, help="0 = heuristic")
     p.add_argument("--no-sweep", action="store_true", help="skip the batch sweep")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-ceiling", action="store_true", help="skip the measured read ceiling")
+    p.add_argument("--no-ragged", action="store_true", help="skip the C3 ragged line")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--trials", type=int, default=15)
     return p.parse_args()
@@ -223,7 +232,45 @@ def main():
             "timed_region_wall_s": round(wall, 4),
         },
     }
+    if not args.no_ceiling:
+        from paged_attention_decode_amd import roofline as rl
+
+        paged_gbs, stream_gbs, details = rl.ceilings(sets, calls=max(20, args.steps // 2))
+        result["roofline"]["measured_ceiling_gbs"] = round(paged_gbs, 1)
+        result["roofline"]["frac_of_measured_ceiling"] = round(value / paged_gbs, 4)
+        result["roofline"]["contiguous_stream_gbs"] = round(stream_gbs, 1)
+        result["roofline"]["ceiling_probe"] = details
     del sets
+
+    if not args.no_ragged:
+        first = wl.make("C3", seed=1000)
+        rs = [first] + [wl.make("C3", seed=1000 + i) for i in range(1, _rotation(first.k_cache.numel() * 4))]
+        calls = max(20, args.steps // 2)
+        dense = _throughput(pad, rs, engine, splits, calls, 10)
+        csr_args = [pad.paged_kv_indices(w.block_table, w.seq_lens, w.k_cache.shape[1]) for w in rs]
+        for i in range(10):
+            j = i % len(rs)
+            pad.paged_attention_decode_csr(rs[j].q, rs[j].k_cache, rs[j].v_cache, *csr_args[j])
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s_ev.record()
+        for i in range(calls):
+            j = i % len(rs)
+            pad.paged_attention_decode_csr(rs[j].q, rs[j].k_cache, rs[j].v_cache, *csr_args[j])
+        e_ev.record()
+        torch.cuda.synchronize()
+        csr = s_ev.elapsed_time(e_ev) / 1e3 / calls
+        nb3 = sum(wl.bytes_of(w) for w in rs) / len(rs)
+        result["c3_ragged"] = {
+            "workload": "C3: batch 32, seq_lens U[1, 8192], GQA 12/2, head_dim 128, page 32; cold "
+                        f"(rotation over {len(rs)} seeded batches)",
+            "us_per_call_dense": round(dense * 1e6, 2),
+            "gbs_dense": round(nb3 / dense / 1e9, 1),
+            "pct_of_peak_dense": round(100 * nb3 / dense / 1e9 / PEAK_GBS, 2),
+            "us_per_call_csr": round(csr * 1e6, 2),
+            "gbs_csr": round(nb3 / csr / 1e9, 1),
+        }
+        del rs, csr_args
 
     if not args.no_sweep:
         sweep = {}

@@ -80,23 +80,20 @@ def _used_pages(w):
 PROBE_SETTINGS = ((4, 2), (8, 1), (8, 2), (4, 4))
 
 
-def measure(name, batch, calls=100, groups=0):
-    sets = _sets(name, batch)
+def ceilings(sets, calls=100, groups=0):
+    """Measured read ceilings for the workloads `sets` (rotated, cold).
+
+    Returns (paged_gbs, stream_gbs, details): the best GB/s over
+    PROBE_SETTINGS of the decode's access pattern without arithmetic, and of
+    a contiguous stream of the same byte count.
+    """
     w0 = sets[0]
     nbytes = wl.bytes_of(w0)
-    flops = wl.flops_of(w0)
     stream = torch.cuda.current_stream().cuda_stream
     lib = probe()
     if groups <= 0:
         groups = torch.cuda.get_device_properties(0).multi_processor_count
     sink = torch.zeros(max(groups, 1), dtype=torch.int32, device="cuda")
-
-    def decode(i):
-        paged_attention_decode(*sets[i].args())
-
-    t_dec = _time(decode, len(sets), calls)
-
-    # The decode's access pattern, arithmetic removed.
     p, ps, hkv, d = w0.k_cache.shape
     pages = [_used_pages(w) for w in sets]
     rows = 16 if ps % 16 == 0 else ps
@@ -129,12 +126,28 @@ def measure(name, batch, calls=100, groups=0):
     for wv, dp in PROBE_SETTINGS:
         us = _time(lambda i: contiguous(i, wv, dp), len(sets), calls)
         stream_rate[(wv, dp)] = span / us / 1e3
-    gbs = nbytes / t_dec / 1e3
     best_paged = max(paged_rate, key=paged_rate.get)
     best_stream = max(stream_rate, key=stream_rate.get)
-    paged_gbs = paged_rate[best_paged]
-    stream_gbs = stream_rate[best_stream]
-    group = w0.q.shape[1] // hkv
+    details = {"groups": groups, "paged_best": {"waves": best_paged[0], "depth": best_paged[1]},
+               "stream_best": {"waves": best_stream[0], "depth": best_stream[1]},
+               "paged_bytes": probe_bytes, "stream_bytes": span}
+    del pages
+    return paged_rate[best_paged], stream_rate[best_stream], details
+
+
+def measure(name, batch, calls=100, groups=0):
+    sets = _sets(name, batch)
+    w0 = sets[0]
+    nbytes = wl.bytes_of(w0)
+    flops = wl.flops_of(w0)
+
+    def decode(i):
+        paged_attention_decode(*sets[i].args())
+
+    t_dec = _time(decode, len(sets), calls)
+    paged_gbs, stream_gbs, details = ceilings(sets, calls, groups)
+    gbs = nbytes / t_dec / 1e3
+    group = w0.q.shape[1] // w0.k_cache.shape[2]
     rec = {
         "config": w0.name,
         "algorithmic_bytes": nbytes,
@@ -148,11 +161,9 @@ def measure(name, batch, calls=100, groups=0):
         "paged_read_gbs": round(paged_gbs, 1),
         "pct_of_paged_read": round(100 * gbs / paged_gbs, 2),
         "stream_read_gbs": round(stream_gbs, 1),
-        "probe": {"groups": groups, "paged_best": {"waves": best_paged[0], "depth": best_paged[1]},
-                  "stream_best": {"waves": best_stream[0], "depth": best_stream[1]},
-                  "paged_bytes": probe_bytes, "stream_bytes": span},
+        "probe": details,
     }
-    del sets, pages
+    del sets
     torch.cuda.empty_cache()
     return rec
 
