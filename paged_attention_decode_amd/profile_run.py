@@ -51,8 +51,10 @@ def main() -> None:
         w = sets[i % n_sets]
         paged_attention_decode_ex(*w.args(), num_splits=a.num_splits or None, engine=a.engine)
     torch.cuda.synchronize()
-    print(f"{w0.name}: {a.calls} calls over {n_sets} input set(s); algorithmic bytes/call {wl.bytes_of(w0)}",
-          flush=True)
+    used = [sets[i % n_sets] for i in range(a.calls)]
+    mean_bytes = sum(wl.bytes_of(w) for w in used) / len(used)
+    print(f"{w0.name}: {a.calls} calls over {n_sets} input set(s); algorithmic bytes/call {wl.bytes_of(w0)} "
+          f"(first set), {mean_bytes:.0f} (mean over the calls)", flush=True)
 
 
 if __name__ == "__main__":
