@@ -221,6 +221,63 @@ __device__ __forceinline__ float2 load_device_f2(__amdgpu_buffer_rsrc_t r, uint3
   return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCachePolicyDevice));
 }
 
+// N consecutive splits' partials of one (row, 4 columns) element, loaded
+// with device-scope loads (the (m, l) pairs first, in split order, then the
+// O vectors) and folded in split order:
+//   m' = max(m, m_s),  l' = l 2^(m - m') + l_s 2^(m_s - m'),
+//   acc' = acc 2^(m - m') + O_s 2^(m_s - m').
+// Every load is unconditional: offsets past the unit's region read as zeros
+// (buffer range check) and are not folded, so the loads of a batch need no
+// branch and each fold step waits only for its own split's data.
+template <int N>
+struct MergeBatch {
+  float2 ml[N];
+  f4_t o[N];
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t o_rsrc, __amdgpu_buffer_rsrc_t ml_rsrc, int sp0,
+                                       int gqa, int row, int col, int d) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) ml[j] = load_device_f2(ml_rsrc, (uint32_t)((sp0 + j) * gqa + row) * 8u);
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      o[j] = load_device_f4(o_rsrc, ((uint32_t)((sp0 + j) * gqa + row) * (uint32_t)d + col) * 4u);
+  }
+  // Splits at or past nsplit fold with m_s = -inf, i.e. weight 0 (their
+  // loads read zeros): the fold has no branch, so the compiler cannot sink a
+  // load into a conditional step and serialise the round trips.  Split 0
+  // always exists, so m is finite before any such step and alpha stays 1.
+  __device__ __forceinline__ void fold(int sp0, int nsplit, float& m, float& l, f4_t& acc) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      // Every published split is non-empty, so its m is finite.
+      const float ms = sp0 + j < nsplit ? ml[j].x : kNegInf;
+      const float m_new = fmaxf(m, ms);
+      const float alpha = exp2_fast(m - m_new);  // 0 while m is -inf
+      const float beta = exp2_fast(ms - m_new);
+      l = l * alpha + ml[j].y * beta;
+      acc = acc * alpha + o[j] * beta;
+      m = m_new;
+    }
+  }
+};
+
+// Folds the partials of splits [0, nsplit) of one element, 8 splits per
+// memory round trip (4 when there are at most 4 splits).
+__device__ __forceinline__ void merge_partials(__amdgpu_buffer_rsrc_t o_rsrc, __amdgpu_buffer_rsrc_t ml_rsrc,
+                                               int nsplit, int gqa, int row, int col, int d, float& m, float& l,
+                                               f4_t& acc) {
+  if (nsplit <= 4) {
+    MergeBatch<4> p;
+    p.load(o_rsrc, ml_rsrc, 0, gqa, row, col, d);
+    p.fold(0, nsplit, m, l, acc);
+    return;
+  }
+  for (int sp0 = 0; sp0 < nsplit; sp0 += 8) {
+    MergeBatch<8> p;
+    p.load(o_rsrc, ml_rsrc, sp0, gqa, row, col, d);
+    p.fold(sp0, nsplit, m, l, acc);
+  }
+}
+
 // Reads an int32 at a wave-uniform address with a scalar load (constant
 // address space): the value lands in an SGPR and its wait counts on the
 // LDS/scalar counter, so it never has to drain the K/V vector loads in
@@ -1053,19 +1110,7 @@ void pad_phase1_kernel(const Phase1Args a) {
     const int col = (e - row * (D / 4)) * 4;
     float m = kNegInf, l = 0.f;
     f4_t acc = (f4_t)0.f;
-#pragma unroll 8
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const uint32_t r = (uint32_t)(sp * gqa + row);
-      const float2 ml = load_device_f2(ml_rsrc, r * 8u);
-      const f4_t o = load_device_f4(o_rsrc, (r * D + col) * 4u);
-      // Every published split is non-empty, so ml.x is finite.
-      const float m_new = fmaxf(m, ml.x);
-      const float alpha = exp2_fast(m - m_new);  // 0 while m is -inf
-      const float beta = exp2_fast(ml.x - m_new);
-      l = l * alpha + ml.y * beta;
-      acc = acc * alpha + o * beta;
-      m = m_new;
-    }
+    merge_partials(o_rsrc, ml_rsrc, nsplit, gqa, row, col, D, m, l, acc);
     const float inv = 1.f / l;
     h4_t hv;
 #pragma unroll
