@@ -121,7 +121,10 @@ typedef struct pad_decode_plan_t {
  * kernel itself reads every sequence length and re-plans the G workgroups
  * over the pages actually in use (equal page chunks, so ragged batches and
  * sequences shorter than max_pages * page_size stay balanced); with every
- * sequence at full capacity that plan is the static one. */
+ * sequence at full capacity that plan is the static one.  A bandwidth-bound
+ * shape with at least one (sequence, kv head) unit per CU gets a grid of 4
+ * items per unit: one item per unit (no partials) when every sequence is at
+ * full capacity, equal page chunks when the lengths are ragged. */
 int pad_decode_plan(const pad_decode_dims* dims, int num_splits, int num_cus,
                     pad_decode_plan_t* plan);
 

@@ -77,7 +77,9 @@ struct Phase1Args {
   int nw;          // waves per workgroup (blockDim.x / 64)
   int ps_shift;    // log2(ps) when ps is a power of two, else -1
   int csr;         // 1: page ids from (indptr, indices, last_page_len)
-  int balance;     // 1: items planned from the sequence lengths in-kernel
+  int balance;     // 1: items planned from the sequence lengths in-kernel;
+                   // 2: the same on an oversubscribed grid (one item per
+                   //    unit when every sequence is full)
   int min_chunk;   // planner: fewest pages per item
   float scale_log2;
   const int32_t* bt;      // dense: block_table [B, max_pages]; CSR: indices
@@ -942,7 +944,10 @@ __device__ __forceinline__ WorkItem static_item(const Phase1Args& a, int s, int 
 }
 
 // Planned mode: read every sequence length; with every sequence at full
-// capacity the static split is already even, otherwise plan the items.
+// capacity the static split is already even (balance == 1) or, on an
+// oversubscribed grid (balance == 2: at least as many (sequence, kv head)
+// units as CUs), each unit is one item of workgroup g = unit and the other
+// workgroups exit; otherwise plan the items.
 template <int NK>
 __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int g, int G, const int32_t* static_row,
                                                  int lane) {
@@ -951,9 +956,27 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int
 #pragma unroll
   for (int k = 0; k < NK; ++k)
     if (lane + 64 * k < a.batch && t.pages[k] != a.max_pages) full = false;
-  if (__builtin_amdgcn_ballot_w64(!full) == 0)
+  if (__builtin_amdgcn_ballot_w64(!full) == 0) {
+    if (a.balance == 2) {
+      WorkItem w;
+      const int units = a.batch * a.hkv;
+      const int u = min(g, units - 1);
+      w.b = u / a.hkv;
+      w.kvh = u - w.b * a.hkv;
+      w.p_begin = 0;
+      w.p_end = a.max_pages;
+      w.L = seq_lane_value<NK>(t.len, w.b);
+      w.nsplit = a.max_pages > 0 ? 1 : 0;
+      w.slot0 = u;
+      w.col_max = a.max_pages - 1;
+      w.valid = g < units;
+      w.ids_row = a.bt + (int64_t)w.b * a.sbb;
+      w.ids_stride = a.sbp;
+      return w;
+    }
     return static_item(a, s, blockIdx.y, blockIdx.z, seq_lane_value<NK>(t.len, blockIdx.z), a.max_pages,
                        static_row, a.sbp);
+  }
   return plan_item<NK>(a, t, g, G, lane);
 }
 
@@ -1171,6 +1194,31 @@ static size_t workspace_layout(const pad_decode_dims* d, int S, void* ws, float*
   return 256 + o_bytes + rows * sizeof(float2);
 }
 
+// Splits per unit on an oversubscribed grid (see oversubscribed_shape).
+constexpr int kOversubscribeSplits = 4;
+
+// A bandwidth-bound shape with at least one (sequence, kv head) unit per CU
+// and a batch the in-kernel planner handles.  One workgroup per unit would
+// be enough for uniform lengths (measured: C2 batch 128 81.4 us with one
+// split against 93.9 us with 4), but ragged ones leave their longest units
+// running alone at the end (C5: 2930 us with one workgroup per unit,
+// 2656 us with kOversubscribeSplits planned items per unit, 2767 us with 8).
+// The launch therefore sizes the grid for kOversubscribeSplits items per
+// unit and the kernel decides from the lengths: all at full capacity, one
+// item per unit; otherwise equal page chunks.
+static bool oversubscribed_shape(const pad_decode_dims* d, int num_splits, int num_cus, bool latency_bound) {
+  const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
+  return num_splits == 0 && !latency_bound && units >= num_cus && d->batch <= kPlanMaxBatch &&
+         d->max_pages < (1 << 23);
+}
+
+static bool latency_bound_shape(const pad_decode_dims* d, int num_cus) {
+  const int max_pages = d->max_pages > 0 ? d->max_pages : 1;
+  const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
+  const int64_t blocks_per_seq = ((int64_t)max_pages * d->page_size + kBlockTokens - 1) / kBlockTokens;
+  return units * blocks_per_seq <= 16 * (int64_t)num_cus;
+}
+
 static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int engine,
                      pad_decode_plan_t* p) {
   const int st = validate_dims(d);
@@ -1189,7 +1237,7 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   // CUs: fewer splits to merge, each streamed by more waves (batch 8: 11.9
   // vs 13.2 us).
   const int64_t blocks_per_seq = ((int64_t)max_pages * d->page_size + kBlockTokens - 1) / kBlockTokens;
-  const bool latency_bound = units * blocks_per_seq <= 16 * (int64_t)num_cus;
+  const bool latency_bound = latency_bound_shape(d, num_cus);
   int S;
   int pps;
   if (num_splits > 0) {
@@ -1205,6 +1253,7 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     const int64_t max_groups = latency_bound ? num_cus / 2 : num_cus;
     int64_t s_want = 1;
     while (s_want * 2 * units <= max_groups) s_want *= 2;
+    if (oversubscribed_shape(d, num_splits, num_cus, latency_bound)) s_want = kOversubscribeSplits;
     int64_t s_cap = blocks_per_seq / kMinBlocks;
     if (s_cap < 1) s_cap = 1;
     if (s_want > s_cap) s_want = s_cap;
@@ -1352,7 +1401,9 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.csr = csr ? 1 : 0;
   // The in-kernel planner evens out ragged batches; an explicit split count
   // keeps its meaning (that many page-aligned splits per sequence).
-  a.balance = (num_splits == 0 && !plan.single_pass && d->batch <= kPlanMaxBatch && d->max_pages < (1 << 23)) ? 1 : 0;
+  a.balance = 0;
+  if (num_splits == 0 && !plan.single_pass && d->batch <= kPlanMaxBatch && d->max_pages < (1 << 23))
+    a.balance = oversubscribed_shape(d, num_splits, cus, latency_bound_shape(d, cus)) ? 2 : 1;
   a.min_chunk = ceil_div(kMinBlocks * kBlockTokens, d->page_size);
   a.ps_shift = -1;
   for (int sh = 0; sh < 31; ++sh)

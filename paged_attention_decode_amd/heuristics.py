@@ -13,7 +13,11 @@ and the CU count.  Fitted to measured split-count sweeps of configurations
 C2 (batch 1-64), C3 and C4 on MI355X: a power-of-two split count with at
 least 16 blocks of 16 tokens per split; bandwidth-bound shapes get one
 4-wave workgroup per CU, latency-bound ones (at most 16 blocks of work per
-CU) 8-wave workgroups on at most half the CUs.
+CU) 8-wave workgroups on at most half the CUs.  Bandwidth-bound shapes with
+at least one (sequence, kv head) unit per CU and batch <= 256 get a grid of
+OVERSUBSCRIBE_SPLITS items per unit, which the kernel fills from the
+lengths: one item per unit when every sequence is full, equal page chunks
+otherwise.
 """
 
 from __future__ import annotations
@@ -25,6 +29,8 @@ MAX_WAVES = 8              # waves per phase-1 workgroup (4 once the CUs are fil
 MAX_SPLITS = 1024          # PAD_MAX_SPLITS
 MIN_BLOCKS = 16            # 16-token blocks per split, at least
 MERGE_LDS_BUDGET = 48 * 1024
+OVERSUBSCRIBE_SPLITS = 4   # items per unit on an oversubscribed grid
+PLAN_MAX_BATCH = 256       # largest batch the in-kernel planner handles
 
 
 @dataclass(frozen=True)
@@ -59,6 +65,8 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
         want = 1
         while want * 2 * units <= max_groups:
             want *= 2
+        if oversubscribed(batch, num_kv_heads, max_pages, latency_bound, num_cus):
+            want = OVERSUBSCRIBE_SPLITS
         cap = max(blocks_per_seq // MIN_BLOCKS, 1)
         want = max(min(want, cap, MAX_SPLITS), 1)
         pps = _cdiv(mp, want)
@@ -71,6 +79,12 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     single = s == 1
     ws = 0 if single else workspace_bytes(batch, num_kv_heads, gqa, head_dim, s)
     return Plan(s, pps, nw, single, ws, 0 if single else batch * num_kv_heads)
+
+
+def oversubscribed(batch: int, num_kv_heads: int, max_pages: int, latency_bound: bool, num_cus: int) -> bool:
+    """Heuristic shape with a unit per CU or more, planned in-kernel over an oversubscribed grid."""
+    return (not latency_bound and max(batch, 1) * num_kv_heads >= num_cus and batch <= PLAN_MAX_BATCH
+            and max_pages < (1 << 23))
 
 
 def workspace_bytes(batch: int, num_kv_heads: int, gqa: int, head_dim: int, num_splits: int) -> int:

@@ -74,6 +74,10 @@ def test_status_strings():
     (1, 12, 2, 128, 16, 1, 8, 256),
     (2, 32, 2, 256, 16, 40, 0, 80),
     (5, 16, 1, 96, 1, 100, 0, 0),
+    (128, 12, 2, 128, 16, 256, 0, 256),
+    (512, 12, 2, 128, 16, 256, 0, 256),
+    (64, 8, 4, 64, 16, 32, 0, 256),
+    (64, 8, 4, 64, 16, 64, 0, 256),
 ])
 def test_plan_matches_python_mirror(batch, hq, hkv, d, ps, max_pages, splits, cus):
     lib = _native.capi()
@@ -105,8 +109,16 @@ def test_heuristic_properties():
         assert p.waves_per_group == 4 and p.num_splits * b * 2 == 256
     p64 = heuristics.plan(64, 12, 2, 128, 16, 256)
     assert p64.num_splits <= 8
+    # At least one unit per CU: a grid of 4 items per unit for the in-kernel
+    # planner (one item per unit if every sequence is full); past the
+    # planner's batch limit, one workgroup per unit.
     p_big = heuristics.plan(256, 64, 8, 128, 16, 2048)
-    assert p_big.num_splits == 1 and p_big.single_pass
+    assert p_big.num_splits == heuristics.OVERSUBSCRIBE_SPLITS and not p_big.single_pass
+    assert p_big.workspace_bytes == heuristics.workspace_bytes(256, 8, 8, 128, heuristics.OVERSUBSCRIBE_SPLITS)
+    p128 = heuristics.plan(128, 12, 2, 128, 16, 256)
+    assert p128.num_splits == heuristics.OVERSUBSCRIBE_SPLITS and p128.waves_per_group == 4
+    p_over = heuristics.plan(512, 12, 2, 128, 16, 256)
+    assert p_over.num_splits == 1 and p_over.single_pass
 
 
 @pytest.mark.parametrize("field,value,code", [

@@ -255,3 +255,42 @@ def test_planner_repeatable():
     first = _run_dense(q, k, v, bt, sl)
     for _ in range(20):
         assert torch.equal(_run_dense(q, k, v, bt, sl), first)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["uniform_full", "full_partial_last_page", "ragged", "ragged_csr"])
+def test_oversubscribed_grid(case):
+    """At least one (sequence, kv head) unit per CU: the launch sizes the grid for 4 items per unit.
+
+    With every sequence at full capacity the kernel gives each unit one item
+    (written straight to the output) and the other workgroups exit; with
+    ragged lengths it plans equal page chunks over the whole grid.
+    """
+    import paged_attention_decode_amd as pad
+
+    batch, ps, hkv, group, d, width = 64, 16, 4, 2, 64, 64
+    assert pad.plan(batch, hkv * group, hkv, d, ps, width)["num_splits"] == 4
+    rng = random.Random(len(case))
+    if case == "uniform_full":
+        lens = [width * ps] * batch
+    elif case == "full_partial_last_page":  # every table row in use, last pages partly filled
+        lens = [width * ps - rng.randint(0, ps - 1) for _ in range(batch)]
+    else:
+        lens = [rng.randint(0, width * ps) for _ in range(batch)]
+        lens[3], lens[10], lens[11] = 0, width * ps, 1
+    bt, num_pages = shuffled_table(lens, ps, spare_pages=3, extra_cols=width - max(cdiv(n, ps) for n in lens),
+                                   seed=len(case))
+    assert bt.shape[1] == width
+    k, v = make_cache(num_pages, ps, hkv, d, seed=len(case))
+    q = torch.randn(batch, hkv * group, d, generator=torch.Generator().manual_seed(3))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    expected = decode_fp16_protocol(q, k, v, bt, sl)
+    if case == "ragged_csr":
+        _check_csr(q, k, v, bt, sl, ps)
+        return
+    out = _run_dense(q, k, v, bt, sl)
+    assert_parity(out, expected)
+    single = _run_dense(q, k, v, bt, sl, num_splits=1)
+    torch.testing.assert_close(out.float(), single.float(), rtol=1e-3, atol=1e-3)
+    for _ in range(5):
+        assert torch.equal(_run_dense(q, k, v, bt, sl), out)
