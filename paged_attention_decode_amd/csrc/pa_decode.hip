@@ -262,8 +262,9 @@ struct MergeBatch {
   }
 };
 
-// Folds the partials of splits [0, nsplit) of one element, 8 splits per
-// memory round trip (4 when there are at most 4 splits).
+// Folds the partials of splits [0, nsplit) of one element, one memory round
+// trip per batch: 4, 8 or 16 splits for split counts up to 4, 8 and 16,
+// batches of 16 beyond.
 __device__ __forceinline__ void merge_partials(__amdgpu_buffer_rsrc_t o_rsrc, __amdgpu_buffer_rsrc_t ml_rsrc,
                                                int nsplit, int gqa, int row, int col, int d, float& m, float& l,
                                                f4_t& acc) {
@@ -273,8 +274,14 @@ __device__ __forceinline__ void merge_partials(__amdgpu_buffer_rsrc_t o_rsrc, __
     p.fold(0, nsplit, m, l, acc);
     return;
   }
-  for (int sp0 = 0; sp0 < nsplit; sp0 += 8) {
+  if (nsplit <= 8) {
     MergeBatch<8> p;
+    p.load(o_rsrc, ml_rsrc, 0, gqa, row, col, d);
+    p.fold(0, nsplit, m, l, acc);
+    return;
+  }
+  for (int sp0 = 0; sp0 < nsplit; sp0 += 16) {
+    MergeBatch<16> p;
     p.load(o_rsrc, ml_rsrc, sp0, gqa, row, col, d);
     p.fold(sp0, nsplit, m, l, acc);
   }
