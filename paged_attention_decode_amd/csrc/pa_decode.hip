@@ -63,6 +63,9 @@ constexpr int kMaxWaves = 8;
 // Fewest 16-token blocks per split (or planned item): each workgroup's fixed
 // costs (q load, wave merge, partial publish) stay small against its streaming.
 constexpr int kMinBlocks = 16;
+// Fewest blocks per split for short latency-bound sequences (split counts up
+// to 16, which one merge round trip covers).
+constexpr int kMinBlocksShort = 4;
 constexpr int kMergeLdsBudget = 48 * 1024;  // bytes of LDS for the wave merge
 // Headroom (base-2 units) a score may exceed the running reference max before
 // the accumulators are rescaled; fp16 weights stay <= 2^8.
@@ -1262,6 +1265,14 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     while (s_want * 2 * units <= max_groups) s_want *= 2;
     if (oversubscribed_shape(d, num_splits, num_cus, latency_bound)) s_want = kOversubscribeSplits;
     int64_t s_cap = blocks_per_seq / kMinBlocks;
+    // Latency-bound short sequences: a wave's serial chain of blocks costs
+    // more than a merge of up to 16 splits (one round trip), so splits may
+    // go down to 4 blocks (C1, 1024 tokens: 9.2 us at 16 splits against
+    // 10.3 us at the 4 that 16-block splits allow).
+    if (latency_bound) {
+      const int64_t short_cap = blocks_per_seq / kMinBlocksShort < 16 ? blocks_per_seq / kMinBlocksShort : 16;
+      if (s_cap < short_cap) s_cap = short_cap;
+    }
     if (s_cap < 1) s_cap = 1;
     if (s_want > s_cap) s_want = s_cap;
     if (s_want > PAD_MAX_SPLITS) s_want = PAD_MAX_SPLITS;

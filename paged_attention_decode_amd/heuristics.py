@@ -28,6 +28,7 @@ BLOCK_TOKENS = 16          # tokens per wave iteration (one MFMA tile)
 MAX_WAVES = 8              # waves per phase-1 workgroup (4 once the CUs are filled)
 MAX_SPLITS = 1024          # PAD_MAX_SPLITS
 MIN_BLOCKS = 16            # 16-token blocks per split, at least
+MIN_BLOCKS_SHORT = 4       # the same for short latency-bound sequences (<= 16 splits)
 MERGE_LDS_BUDGET = 48 * 1024
 OVERSUBSCRIBE_SPLITS = 4   # items per unit on an oversubscribed grid
 PLAN_MAX_BATCH = 256       # largest batch the in-kernel planner handles
@@ -67,7 +68,10 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
             want *= 2
         if oversubscribed(batch, num_kv_heads, max_pages, latency_bound, num_cus):
             want = OVERSUBSCRIBE_SPLITS
-        cap = max(blocks_per_seq // MIN_BLOCKS, 1)
+        cap = blocks_per_seq // MIN_BLOCKS
+        if latency_bound:  # short sequences: down to 4 blocks per split, at most 16 splits
+            cap = max(cap, min(blocks_per_seq // MIN_BLOCKS_SHORT, 16))
+        cap = max(cap, 1)
         want = max(min(want, cap, MAX_SPLITS), 1)
         pps = _cdiv(mp, want)
         s = _cdiv(mp, pps)
