@@ -14,6 +14,8 @@ from __future__ import annotations
 
 import os
 
+import random
+
 import pytest
 import torch
 
@@ -254,6 +256,35 @@ def test_runs_on_current_stream():
         assert_parity(o, expected)
 
 
+def test_concurrent_streams_keep_their_own_scratch():
+    # Two streams decode different batches at the same time; the binding
+    # keeps split scratch (partials and arrival counters) per stream, so the
+    # interleaved launches must not disturb each other.
+    import paged_attention_decode_amd as pad
+
+    cases = []
+    for lens, seed in (([4096, 4096, 3000], 81), ([2500, 17, 4096, 900, 1], 82)):
+        bt, n = shuffled_table(lens, 16, spare_pages=1, extra_cols=0, seed=seed)
+        k, v = make_cache(n, 16, 2, 128, seed=seed)
+        q = torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(seed))
+        sl = torch.tensor(lens, dtype=torch.int32)
+        cases.append(([q.half().cuda(), k.half().cuda(), v.half().cuda(), bt.cuda(), sl.cuda()],
+                      decode_fp16_protocol(q, k, v, bt, sl)))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[], []]
+    for _ in range(20):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                outs[i].append(pad.paged_attention_decode(*cases[i][0]))
+    for st in streams:
+        st.synchronize()
+    for i in range(2):
+        assert_parity(outs[i][0], cases[i][1])
+        for o in outs[i][1:]:
+            assert torch.equal(o, outs[i][0])
+
+
 def test_mixed_call_shapes_share_scratch():
     # Calls of different shapes reuse the binding's per-stream scratch: a call
     # with few long sequences (many partials) followed by calls with many
@@ -261,7 +292,11 @@ def test_mixed_call_shapes_share_scratch():
     import paged_attention_decode_amd as pad
 
     cases = []
-    for lens, seed in (([4000, 3000], 71), ([300] * 100, 72), ([1500] * 7, 73), ([64] * 300, 74)):
+    # ... and so do oversubscribed grids (at least one (sequence, kv head)
+    # unit per CU): a full batch (one item per unit) and a ragged one.
+    ragged = [random.Random(75).randint(0, 1200) for _ in range(150)]
+    for lens, seed in (([4000, 3000], 71), ([300] * 100, 72), ([1500] * 7, 73), ([64] * 300, 74),
+                       ([1200] * 150, 75), (ragged, 76)):
         bt, n = shuffled_table(lens, 16, spare_pages=1, extra_cols=0, seed=seed)
         k, v = make_cache(n, 16, 2, 128, seed=seed)
         q = torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(seed))
