@@ -344,7 +344,16 @@ __device__ __forceinline__ int first_page_id(const Phase1Args& a, const int32_t*
   return load_uniform_i32(ids_row + (int64_t)col * ids_stride);
 }
 
-template <int D, bool UNIFORM>
+// Block-addressing modes of the MFMA wave loop (template parameter MODE):
+//   kModeGeneric  any page size: each token looks up its own page;
+//   kModeUniform  page_size % 16 == 0: a 16-token block lies in one page;
+//   kModeSubpage + s  page_size = 2^s < 16: a block covers 16 >> s whole
+//                 pages (items start on page boundaries).
+constexpr int kModeGeneric = 0;
+constexpr int kModeUniform = 1;
+constexpr int kModeSubpage = 2;
+
+template <int D, int MODE>
 __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_first, const int32_t* bt_row,
                                                int64_t ids_stride, int b, int kvh, int t_begin, int t_end,
                                                int nblk, int wave, int nw, int lane, float2* sm_ml, float* sm_o,
@@ -380,23 +389,41 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   // 4g+i, head_dim slice r16*DT, so one load instruction covers four full
   // rows (contiguous 256 B each at head_dim 128).  K then goes through LDS
   // into the MFMA operand layout (token per lane%16).
+  // Sub-page blocks: token 4g+i sits in slot (4g+i) mod page_size of its
+  // page (blocks start on page boundaries), again loop invariant.
+  constexpr int SUB_SHIFT = MODE >= kModeSubpage ? MODE - kModeSubpage : 0;
+  constexpr int SUB_PAGES = 16 >> SUB_SHIFT;  // pages per 16-token block
   uint32_t koff[4], voff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    koff[i] = (uint32_t)(((int64_t)(4 * g + i) * a.sks + r16 * DT) * 2);
-    voff[i] = (uint32_t)(((int64_t)(4 * g + i) * a.svs + r16 * DT) * 2);
+    const int row = MODE >= kModeSubpage ? (4 * g + i) & ((1 << SUB_SHIFT) - 1) : 4 * g + i;
+    koff[i] = (uint32_t)(((int64_t)row * a.sks + r16 * DT) * 2);
+    voff[i] = (uint32_t)(((int64_t)row * a.svs + r16 * DT) * 2);
   }
   constexpr int KROW = k_stage_row_bytes<D>();
   const int p_first = page_of(a, t_begin);
+  // Sub-page blocks: the raw page ids of the block the next load() reads,
+  // read with scalar loads one block ahead like pid_next; columns past the
+  // item's last page are clamped to it (its tokens are masked).
+  int ids_next[MODE >= kModeSubpage ? SUB_PAGES : 1];
+  const int p_last = t_end > t_begin ? page_of(a, t_end - 1) : p_first;
+  auto fetch_ids = [&](int jb) {
+    if constexpr (MODE >= kModeSubpage) {
+      const int p0 = p_first + jb * SUB_PAGES;
+#pragma unroll
+      for (int k = 0; k < SUB_PAGES; ++k)
+        ids_next[k] = load_uniform_i32(bt_row + (int64_t)min(p0 + k, p_last) * ids_stride);
+    }
+  };
 
-  // UNIFORM: raw page id of the block the next load() reads.  Each load()
+  // Uniform mode: raw page id of the block the next load() reads.  Each load()
   // consumes it and issues the scalar read of the following block's id, so
   // that read is in flight during a whole compute() (calls come in block
   // order wave, wave+nw, ...; past the split the last block's id is reread).
   int pid_next = phys_first;
 
   auto load = [&](KVTile<D>& t, int jb) {
-    if constexpr (UNIFORM) {
+    if constexpr (MODE == kModeUniform) {
       // page_size % 16 == 0 and splits start on page boundaries: the block
       // lives in one page, so its page id and base address are wave-uniform.
       const int jp = block_page(a, jb);
@@ -410,6 +437,25 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
       for (int i = 0; i < 4; ++i) t.k[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(kb + koff[i]));
 #pragma unroll
       for (int i = 0; i < 4; ++i) t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(vb + voff[i]));
+    } else if constexpr (MODE >= kModeSubpage) {
+      // page_size divides 16: the block covers SUB_PAGES whole pages whose
+      // ids arrived during the previous compute(); lane group g picks the
+      // page of its token 4g+i.  Past the item's end the clamped ids still
+      // name valid pages (the tokens are masked in compute).
+      // The ids are used up before the next block's are fetched into the
+      // same registers.
+#pragma unroll
+      for (int k = 0; k < SUB_PAGES; ++k) ids_next[k] = clamp_page(ids_next[k], a.num_pages);
+      const int64_t kpage = a.skp * 2, vpage = a.svp * 2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c0 = ids_next[i >> SUB_SHIFT], c1 = ids_next[(4 + i) >> SUB_SHIFT];
+        const int c2 = ids_next[(8 + i) >> SUB_SHIFT], c3 = ids_next[(12 + i) >> SUB_SHIFT];
+        const int phys = g == 0 ? c0 : (g == 1 ? c1 : (g == 2 ? c2 : c3));
+        t.k[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(k_head + (int64_t)phys * kpage + koff[i]));
+        t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(v_head + (int64_t)phys * vpage + voff[i]));
+      }
+      fetch_ids(min(jb + nw, nblk - 1));
     } else {
       // Any page size: each token looks up its own page; tokens past the
       // end are clamped to the last valid token (and masked in compute).
@@ -509,6 +555,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   KVTile<D> ta, tb;
   if (n_mine > 0) {
     int it = 0;
+    fetch_ids(wave);
     load(ta, wave);
     load_q();
     for (; it + 2 < n_mine; it += 2) {
@@ -998,7 +1045,7 @@ constexpr int phase1_waves_per_simd(int d, int engine) {
 }
 
 // Phase 1: one workgroup per (split, kv head, sequence).
-template <int D, bool UNIFORM, int ENGINE, int GQA_T>
+template <int D, int MODE, int ENGINE, int GQA_T>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE))))
 void pad_phase1_kernel(const Phase1Args a) {
   extern __shared__ float4 smem_f4[];
@@ -1019,7 +1066,7 @@ void pad_phase1_kernel(const Phase1Args a) {
   // item turns out to be the static one.
   const int32_t* static_row = a.bt + (int64_t)blockIdx.z * a.sbb;
   int phys_first = 0;
-  if constexpr (ENGINE == 0 && UNIFORM) {
+  if constexpr (ENGINE == 0 && MODE == kModeUniform) {
     if (!a.csr) phys_first = first_page_id(a, static_row, a.sbp, a.max_pages - 1, s * a.pps, wave);
   }
   // Read unconditionally (any valid word when unused) after the page id, so
@@ -1054,7 +1101,7 @@ void pad_phase1_kernel(const Phase1Args a) {
     }
     return;
   }
-  if constexpr (ENGINE == 0 && UNIFORM) {
+  if constexpr (ENGINE == 0 && MODE == kModeUniform) {
     if (a.csr || b != (int)blockIdx.z || it.p_begin != s * a.pps)
       phys_first = first_page_id(a, it.ids_row, it.ids_stride, it.col_max, it.p_begin, wave);
   }
@@ -1063,10 +1110,10 @@ void pad_phase1_kernel(const Phase1Args a) {
   const int nblk = (t_end - t_begin + kBlockTokens - 1) / kBlockTokens;
 
   if constexpr (ENGINE == 0) {
-    wave_loop_mfma<D, UNIFORM>(a, phys_first, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw,
+    wave_loop_mfma<D, MODE>(a, phys_first, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw,
                                lane, sm_ml, sm_o, k_stage_all + wave * k_stage_bytes<D>());
   } else {
-    wave_loop_valu<D, UNIFORM, GQA_T>(a, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw, lane,
+    wave_loop_valu<D, MODE == kModeUniform, GQA_T>(a, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw, lane,
                                       sm_ml, sm_o);
   }
   __syncthreads();
@@ -1317,33 +1364,44 @@ static int device_cus(int* out) {
   return PAD_OK;
 }
 
-template <int D, bool UNIFORM, int ENGINE, int GQA_T>
+template <int D, int MODE, int ENGINE, int GQA_T>
 static hipError_t launch_p1(const Phase1Args& a, dim3 grid, int nw, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((pad_phase1_kernel<D, UNIFORM, ENGINE, GQA_T>), grid, dim3(nw * 64), lds, st, a);
+  hipLaunchKernelGGL((pad_phase1_kernel<D, MODE, ENGINE, GQA_T>), grid, dim3(nw * 64), lds, st, a);
   return hipGetLastError();
 }
 
-template <int D, bool UNIFORM>
+template <int D, int MODE>
 static hipError_t dispatch_engine(const Phase1Args& a, dim3 grid, int nw, size_t lds, int engine,
                                   hipStream_t st) {
   if (engine == 1) {
-    if constexpr (D == 64 || D == 128) {
-      if (a.gqa == 1) return launch_p1<D, UNIFORM, 1, 1>(a, grid, nw, lds, st);
-      if (a.gqa == 2) return launch_p1<D, UNIFORM, 1, 2>(a, grid, nw, lds, st);
-      if (a.gqa <= 4) return launch_p1<D, UNIFORM, 1, 4>(a, grid, nw, lds, st);
-      if (a.gqa <= 6) return launch_p1<D, UNIFORM, 1, 6>(a, grid, nw, lds, st);
-      return launch_p1<D, UNIFORM, 1, 8>(a, grid, nw, lds, st);
+    if constexpr ((D == 64 || D == 128) && MODE <= kModeUniform) {
+      if (a.gqa == 1) return launch_p1<D, MODE, 1, 1>(a, grid, nw, lds, st);
+      if (a.gqa == 2) return launch_p1<D, MODE, 1, 2>(a, grid, nw, lds, st);
+      if (a.gqa <= 4) return launch_p1<D, MODE, 1, 4>(a, grid, nw, lds, st);
+      if (a.gqa <= 6) return launch_p1<D, MODE, 1, 6>(a, grid, nw, lds, st);
+      return launch_p1<D, MODE, 1, 8>(a, grid, nw, lds, st);
     }
     return hipErrorInvalidValue;
   }
-  return launch_p1<D, UNIFORM, 0, 0>(a, grid, nw, lds, st);
+  return launch_p1<D, MODE, 0, 0>(a, grid, nw, lds, st);
 }
 
+// Block-addressing mode from the page size (the VALU engine has the uniform
+// and generic modes only).
 template <int D>
 static hipError_t dispatch_phase1(const Phase1Args& a, dim3 grid, int nw, size_t lds, int engine,
                                   hipStream_t st) {
-  if (a.ps % kBlockTokens == 0) return dispatch_engine<D, true>(a, grid, nw, lds, engine, st);
-  return dispatch_engine<D, false>(a, grid, nw, lds, engine, st);
+  if (a.ps % kBlockTokens == 0) return dispatch_engine<D, kModeUniform>(a, grid, nw, lds, engine, st);
+  if (engine == 0) {
+    switch (a.ps) {
+      case 1: return dispatch_engine<D, kModeSubpage + 0>(a, grid, nw, lds, engine, st);
+      case 2: return dispatch_engine<D, kModeSubpage + 1>(a, grid, nw, lds, engine, st);
+      case 4: return dispatch_engine<D, kModeSubpage + 2>(a, grid, nw, lds, engine, st);
+      case 8: return dispatch_engine<D, kModeSubpage + 3>(a, grid, nw, lds, engine, st);
+      default: break;
+    }
+  }
+  return dispatch_engine<D, kModeGeneric>(a, grid, nw, lds, engine, st);
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

@@ -294,3 +294,21 @@ def test_oversubscribed_grid(case):
     torch.testing.assert_close(out.float(), single.float(), rtol=1e-3, atol=1e-3)
     for _ in range(5):
         assert torch.equal(_run_dense(q, k, v, bt, sl), out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ps", [1, 2, 4, 8])
+def test_subpage_blocks_ragged_planned(ps):
+    """Page sizes dividing 16: each 16-token block spans 16 / page_size pages read by page id in registers.
+
+    Ragged lengths (partial last blocks and pages, an empty row, one row of a
+    single token) on shuffled pages, through the planner, a static split and
+    the CSR entry.
+    """
+    rng = random.Random(100 + ps)
+    lens = [rng.randint(1, 3000) for _ in range(10)] + [0, 1, 16 * 40 + 3]
+    q, k, v, bt, sl = _dense(lens, ps=ps, hkv=2, group=4, d=128, extra_cols=2, seed=100 + ps)
+    expected = decode_fp16_protocol(q, k, v, bt, sl)
+    assert_parity(_run_dense(q, k, v, bt, sl), expected)
+    assert_parity(_run_dense(q, k, v, bt, sl, num_splits=5), expected)
+    _check_csr(q, k, v, bt, sl, ps)

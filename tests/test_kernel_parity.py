@@ -170,7 +170,7 @@ def test_poisoned_holes_and_nan_slots(engine):
 
 
 @pytest.mark.parametrize("engine", ENGINES)
-@pytest.mark.parametrize("ps", [1, 4, 8, 12, 16, 32, 64])
+@pytest.mark.parametrize("ps", [1, 2, 4, 8, 12, 16, 32, 64])
 def test_page_sizes(engine, ps):
     lens = [1, ps + 3, 150, 77]
     bt, n = shuffled_table(lens, ps, spare_pages=2, extra_cols=1, seed=ps)
