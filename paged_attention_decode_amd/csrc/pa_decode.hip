@@ -84,6 +84,7 @@ struct Phase1Args {
                    // 2: the same on an oversubscribed grid (one item per
                    //    unit when every sequence is full)
   int min_chunk;   // planner: fewest pages per item
+  int pair_heads;  // 1: workgroups 8 apart take kv heads 2m and 2m+1 (see grid_pos)
   float scale_log2;
   const int32_t* bt;      // dense: block_table [B, max_pages]; CSR: indices
   const int32_t* sl;      // dense: seq_lens [B]
@@ -193,6 +194,14 @@ __device__ __forceinline__ HVec<NDW> load_hvec_stream(const _Float16* p) {
     for (int i = 0; i < NDW / 2; ++i) {
       const u2_t x = __builtin_nontemporal_load(reinterpret_cast<const u2_t*>(p) + i);
       r.w[2 * i + 0] = x[0]; r.w[2 * i + 1] = x[1];
+    }
+  } else if constexpr (NDW % 3 == 0) {
+    // head_dim 96: 12-byte row segments, one 3-dword load each.
+    typedef uint32_t u3_t __attribute__((ext_vector_type(3)));
+#pragma unroll
+    for (int i = 0; i < NDW / 3; ++i) {
+      const u3_t x = __builtin_nontemporal_load(reinterpret_cast<const u3_t*>(p) + i);
+      r.w[3 * i + 0] = x[0]; r.w[3 * i + 1] = x[1]; r.w[3 * i + 2] = x[2];
     }
   } else {
 #pragma unroll
@@ -729,13 +738,13 @@ __device__ __forceinline__ void wave_loop_valu(const Phase1Args& a, const int32_
 }
 
 // ---------------------------------------------------------------------------
-// Work items.  Workgroup g of the grid (g = blockIdx.x + S*(blockIdx.y +
-// Hkv*blockIdx.z)) processes one item: a page range of one (sequence, kv
-// head) unit, and writes its partial to slot g of the workspace.  The items
-// of a unit occupy the consecutive slots [slot0, slot0 + nsplit).
+// Work items.  Workgroup (s, h, b) of the grid (grid_pos: the grid
+// coordinates, or a bijection of them that pairs kv heads on an XCD) has
+// index g = s + S*(h + Hkv*b) and processes one item: a page range of one
+// (sequence, kv head) unit, writing its partial to slot g of the workspace.
+// The items of a unit occupy the consecutive slots [slot0, slot0 + nsplit).
 //  * Static items (an explicit split count, or every sequence at full
-//    capacity): item g is split blockIdx.x of unit (blockIdx.z, blockIdx.y),
-//    pages [s*pps, (s+1)*pps).
+//    capacity): item g is split s of unit (b, h), pages [s*pps, (s+1)*pps).
 //  * Planned items (heuristic split count, batch <= kPlanMaxBatch): every
 //    workgroup reads all sequence lengths and computes the same plan - the
 //    smallest chunk of c pages (c >= min_chunk) such that the units need at
@@ -1006,8 +1015,8 @@ __device__ __forceinline__ WorkItem static_item(const Phase1Args& a, int s, int 
 // units as CUs), each unit is one item of workgroup g = unit and the other
 // workgroups exit; otherwise plan the items.
 template <int NK>
-__device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int g, int G, const int32_t* static_row,
-                                                 int lane) {
+__device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int h, int bz, int g, int G, int lin,
+                                                 const int32_t* static_row, int lane) {
   const SeqTable<NK> t = load_seq_table<NK>(a, lane);
   bool full = !a.csr;
 #pragma unroll
@@ -1017,7 +1026,11 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int
     if (a.balance == 2) {
       WorkItem w;
       const int units = a.batch * a.hkv;
-      const int u = min(g, units - 1);
+      // With pair_heads, units 2r and 2r+1 (kv heads 2m, 2m+1 of one
+      // sequence) go to workgroups 8 apart, as grid_pos does for splits.
+      const bool paired = a.pair_heads && units % 16 == 0;
+      const int gu = paired ? 2 * (((lin >> 4) << 3) | (lin & 7)) + ((lin >> 3) & 1) : g;
+      const int u = min(paired ? (lin < units ? gu : units - 1) : g, units - 1);
       w.b = u / a.hkv;
       w.kvh = u - w.b * a.hkv;
       w.p_begin = 0;
@@ -1026,13 +1039,12 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int
       w.nsplit = a.max_pages > 0 ? 1 : 0;
       w.slot0 = u;
       w.col_max = a.max_pages - 1;
-      w.valid = g < units;
+      w.valid = (paired ? lin : g) < units;
       w.ids_row = a.bt + (int64_t)w.b * a.sbb;
       w.ids_stride = a.sbp;
       return w;
     }
-    return static_item(a, s, blockIdx.y, blockIdx.z, seq_lane_value<NK>(t.len, blockIdx.z), a.max_pages,
-                       static_row, a.sbp);
+    return static_item(a, s, h, bz, seq_lane_value<NK>(t.len, bz), a.max_pages, static_row, a.sbp);
   }
   return plan_item<NK>(a, t, g, G, lane);
 }
@@ -1042,6 +1054,30 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int
 // grid to one round of resident waves using the same numbers.
 constexpr int phase1_waves_per_simd(int d, int engine) {
   return engine == 0 ? (d <= 128 ? 3 : 1) : 1;
+}
+
+// The (split, kv head, sequence) of this workgroup.  Normally the grid
+// coordinates.  With pair_heads (head_dim rows that are not a multiple of
+// 128 bytes, so kv heads 2m and 2m+1 share a cache line in every token
+// slot; an even head count; G a multiple of 16) linear workgroup L takes
+// head parity (L / 8) mod 2 and the rest of its position from the other
+// bits: the two workgroups of a head pair are 8 apart, which the dispatcher
+// places on the same XCD one after the other, so the line they share is
+// fetched into that XCD's L2 once.  Any bijection of the grid is correct;
+// this one only changes what shares a cache.
+__device__ __forceinline__ void grid_pos(const Phase1Args& a, int& s, int& h, int& bz, int& lin) {
+  s = blockIdx.x;
+  h = blockIdx.y;
+  bz = blockIdx.z;
+  lin = blockIdx.x + a.num_splits * (blockIdx.y + a.hkv * blockIdx.z);
+  if (a.pair_heads) {
+    const int rest = ((lin >> 4) << 3) | (lin & 7);
+    const int q = rest / a.num_splits;
+    const int half = a.hkv >> 1;
+    s = rest - q * a.num_splits;
+    bz = q / half;
+    h = 2 * (q - bz * half) + ((lin >> 3) & 1);
+  }
 }
 
 // Phase 1: one workgroup per (split, kv head, sequence).
@@ -1055,37 +1091,37 @@ void pad_phase1_kernel(const Phase1Args a) {
   // [nw] K staging tiles (MFMA engine), after the wave states.
   char* k_stage_all = reinterpret_cast<char*>(sm_o + nw * a.gqa * wave_row_floats<D>());
 
-  const int s = blockIdx.x;
+  int s, h, bz, lin;
+  grid_pos(a, s, h, bz, lin);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = blockIdx.x + a.num_splits * (blockIdx.y + a.hkv * blockIdx.z);
+  const int g = s + a.num_splits * (h + a.hkv * bz);
   const int G = a.num_splits * a.hkv * a.batch;
 
   // Dense page table: read the first page id of this workgroup's static
   // split before the sequence lengths arrive; it stays valid whenever the
   // item turns out to be the static one.
-  const int32_t* static_row = a.bt + (int64_t)blockIdx.z * a.sbb;
+  const int32_t* static_row = a.bt + (int64_t)bz * a.sbb;
   int phys_first = 0;
   if constexpr (ENGINE == 0 && MODE == kModeUniform) {
     if (!a.csr) phys_first = first_page_id(a, static_row, a.sbp, a.max_pages - 1, s * a.pps, wave);
   }
   // Read unconditionally (any valid word when unused) after the page id, so
   // both reads share one round trip.
-  const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)blockIdx.z * a.ssl);
+  const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)bz * a.ssl);
   WorkItem it;
   if (a.balance) {
     if (a.batch <= 64)
-      it = resolve_item<1>(a, s, g, G, static_row, lane);
+      it = resolve_item<1>(a, s, h, bz, g, G, lin, static_row, lane);
     else
-      it = resolve_item<4>(a, s, g, G, static_row, lane);
+      it = resolve_item<4>(a, s, h, bz, g, G, lin, static_row, lane);
   } else if (a.csr) {
-    const int b = blockIdx.z;
     int row, pages, L;
-    csr_row(a, b, &row, &pages, &L);
-    it = static_item(a, s, blockIdx.y, b, L, pages, a.bt + row, 1);
+    csr_row(a, bz, &row, &pages, &L);
+    it = static_item(a, s, h, bz, L, pages, a.bt + row, 1);
   } else {
     const int L = max(static_len, 0);
-    it = static_item(a, s, blockIdx.y, blockIdx.z, L, min(pages_for(a, L), a.max_pages), static_row, a.sbp);
+    it = static_item(a, s, h, bz, L, min(pages_for(a, L), a.max_pages), static_row, a.sbp);
   }
   if (!it.valid) return;
   const int b = it.b;
@@ -1102,7 +1138,7 @@ void pad_phase1_kernel(const Phase1Args a) {
     return;
   }
   if constexpr (ENGINE == 0 && MODE == kModeUniform) {
-    if (a.csr || b != (int)blockIdx.z || it.p_begin != s * a.pps)
+    if (a.csr || b != bz || it.p_begin != s * a.pps)
       phys_first = first_page_id(a, it.ids_row, it.ids_stride, it.col_max, it.p_begin, wave);
   }
   const int t_begin = it.p_begin * a.ps;
@@ -1330,7 +1366,13 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   // merge's LDS allows.
   const int64_t split_tokens = (int64_t)pps * d->page_size;
   int nw = (int)((split_tokens + kBlockTokens - 1) / kBlockTokens);
-  const int nw_max = latency_bound ? kMaxWaves : kMaxWaves / 2;
+  // Bandwidth-bound shapes run 4 waves per workgroup, except head_dim <= 64
+  // on a grid of one workgroup per CU: its 16-token tiles are half the bytes
+  // or less, and 8 waves keep as many bytes in flight per CU (32/8 d64 batch
+  // 32: 25.8 against 29.9 us; 16/4 d32: 17.8 against 21.9 us).  On an
+  // oversubscribed grid 4-wave workgroups let several units share a CU.
+  const bool narrow_rows = d->head_dim <= 64 && !oversubscribed_shape(d, num_splits, num_cus, latency_bound);
+  const int nw_max = (latency_bound || narrow_rows) ? kMaxWaves : kMaxWaves / 2;
   if (nw > nw_max) nw = nw_max;
   const int cap = merge_wave_cap(gqa, d->head_dim);
   if (nw > cap) nw = cap;
@@ -1481,6 +1523,8 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   if (num_splits == 0 && !plan.single_pass && d->batch <= kPlanMaxBatch && d->max_pages < (1 << 23))
     a.balance = oversubscribed_shape(d, num_splits, cus, latency_bound_shape(d, cus)) ? 2 : 1;
   a.min_chunk = ceil_div(kMinBlocks * kBlockTokens, d->page_size);
+  a.pair_heads = ((d->head_dim * 2) % 128 != 0 && d->num_kv_heads % 2 == 0 &&
+                  ((int64_t)S * d->num_kv_heads * d->batch) % 16 == 0) ? 1 : 0;
   a.ps_shift = -1;
   for (int sh = 0; sh < 31; ++sh)
     if ((1 << sh) == d->page_size) a.ps_shift = sh;

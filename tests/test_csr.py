@@ -312,3 +312,27 @@ def test_subpage_blocks_ragged_planned(ps):
     assert_parity(_run_dense(q, k, v, bt, sl), expected)
     assert_parity(_run_dense(q, k, v, bt, sl, num_splits=5), expected)
     _check_csr(q, k, v, bt, sl, ps)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", [32, 96])
+@pytest.mark.parametrize("case", ["static_full", "oversubscribed_full", "ragged", "explicit_splits"])
+def test_head_pair_placement(d, case):
+    """Rows that are not a multiple of 128 bytes (head_dim 32, 96): kv heads 2m and 2m+1 share a
+    cache line per token slot, so the kernel places their workgroups 8 apart (same XCD); the
+    placement is a bijection of the grid, so every path must still match the oracle."""
+    ps, hkv, group = 16, 8, 2
+    if case == "oversubscribed_full":
+        lens = [512] * 32              # 256 (sequence, kv head) units: one per CU or more
+    elif case == "ragged":
+        rng = random.Random(d)
+        lens = [rng.randint(1, 1500) for _ in range(8)]
+    else:
+        lens = [1024] * 8
+    q, k, v, bt, sl = _dense(lens, ps=ps, hkv=hkv, group=group, d=d, seed=d + len(case))
+    expected = decode_fp16_protocol(q, k, v, bt, sl)
+    splits = 3 if case == "explicit_splits" else None
+    out = _run_dense(q, k, v, bt, sl, num_splits=splits)
+    assert_parity(out, expected)
+    for _ in range(3):
+        assert torch.equal(_run_dense(q, k, v, bt, sl, num_splits=splits), out)
