@@ -285,6 +285,45 @@ def test_concurrent_streams_keep_their_own_scratch():
             assert torch.equal(o, outs[i][0])
 
 
+def test_graph_capture_replays():
+    # Serving engines capture the decode in a HIP graph and replay it with
+    # new inputs written in place.  The launch allocates nothing once its
+    # stream's scratch exists, the split merge leaves its arrival counters at
+    # zero, and the workspace carries no state, so every replay must equal an
+    # eager call on the same inputs - with eager decodes (other scratch) run
+    # between the replays.
+    import paged_attention_decode_amd as pad
+
+    lens = [4096, 300, 2500, 1]
+    bt, n = shuffled_table(lens, 16, spare_pages=1, extra_cols=1, seed=91)
+    k, v = make_cache(n, 16, 2, 128, seed=91)
+    dev = [k.half().cuda(), v.half().cuda(), bt.cuda(), torch.tensor(lens, dtype=torch.int32).cuda()]
+    qs = [torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(92 + i)).half().cuda()
+          for i in range(4)]
+    q_static = qs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):  # allocates this stream's scratch before capture
+            pad.paged_attention_decode(q_static, *dev)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out_static = pad.paged_attention_decode(q_static, *dev)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for q in qs:
+            q_static.copy_(q)
+            graph.replay()
+            torch.cuda.synchronize()
+            eager = pad.paged_attention_decode(q, *dev)
+            torch.cuda.synchronize()
+            assert torch.equal(out_static, eager), f"replay {rep} differs from the eager call"
+    assert_parity(out_static, decode_fp16_protocol(qs[-1].float().cpu(), k, v, bt,
+                                                   torch.tensor(lens, dtype=torch.int32)))
+
+
 def test_mixed_call_shapes_share_scratch():
     # Calls of different shapes reuse the binding's per-stream scratch: a call
     # with few long sequences (many partials) followed by calls with many
