@@ -1367,11 +1367,12 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   const int64_t split_tokens = (int64_t)pps * d->page_size;
   int nw = (int)((split_tokens + kBlockTokens - 1) / kBlockTokens);
   // Bandwidth-bound shapes run 4 waves per workgroup, except head_dim <= 64
-  // on a grid of one workgroup per CU: its 16-token tiles are half the bytes
-  // or less, and 8 waves keep as many bytes in flight per CU (32/8 d64 batch
-  // 32: 25.8 against 29.9 us; 16/4 d32: 17.8 against 21.9 us).  On an
-  // oversubscribed grid 4-wave workgroups let several units share a CU.
-  const bool narrow_rows = d->head_dim <= 64 && !oversubscribed_shape(d, num_splits, num_cus, latency_bound);
+  // with at most one (sequence, kv head) unit per CU: its 16-token tiles are
+  // half the bytes or less, and 8 waves keep as many bytes in flight per CU
+  // (32/8 d64 batch 32: 25.8 against 29.9 us; 16/4 d32: 17.8 against 21.9
+  // us).  With more units than CUs, 4-wave workgroups let several units
+  // share a CU (16/16 d64 batch 32: 46.9 against 47.9 us).
+  const bool narrow_rows = d->head_dim <= 64 && units <= num_cus;
   const int nw_max = (latency_bound || narrow_rows) ? kMaxWaves : kMaxWaves / 2;
   if (nw > nw_max) nw = nw_max;
   const int cap = merge_wave_cap(gqa, d->head_dim);

@@ -76,8 +76,7 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
         pps = _cdiv(mp, want)
         s = _cdiv(mp, pps)
     nw = _cdiv(pps * page_size, BLOCK_TOKENS)
-    narrow_rows = head_dim <= 64 and not (num_splits == 0 and oversubscribed(batch, num_kv_heads, max_pages,
-                                                                             latency_bound, num_cus))
+    narrow_rows = head_dim <= 64 and units <= num_cus
     nw = min(nw, MAX_WAVES if latency_bound or narrow_rows else MAX_WAVES // 2)
     per_wave = 16 * 8 + gqa * (head_dim + 4) * 4
     cap_w = max(min(MERGE_LDS_BUDGET // per_wave, MAX_WAVES), 1)

@@ -57,3 +57,12 @@ def test_split_sweep_small():
     assert all(r["us_per_call"] > 0 for r in res["rows"])
     assert res["heuristic_plan"]["num_splits"] >= 1
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+def test_shape_survey_small():
+    from paged_attention_decode_amd import sweep
+
+    rows = sweep.survey(cases=[(2, 12, 2, 128, 4, 256), (2, 8, 4, 96, 16, 256)], calls=3, reps=1)
+    assert [r["page_size"] for r in rows] == [4, 16]
+    assert all(r["us_per_call"] > 0 and 0 < r["gbs"] < 8000 for r in rows)
