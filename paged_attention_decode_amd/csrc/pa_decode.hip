@@ -354,7 +354,7 @@ __device__ __forceinline__ int first_page_id(const Phase1Args& a, const int32_t*
 }
 
 // Block-addressing modes of the MFMA wave loop (template parameter MODE):
-//   kModeGeneric  any page size: each token looks up its own page;
+//   kModeGeneric  any other page size (>= 3): a block spans up to 6 pages;
 //   kModeUniform  page_size % 16 == 0: a 16-token block lies in one page;
 //   kModeSubpage + s  page_size = 2^s < 16: a block covers 16 >> s whole
 //                 pages (items start on page boundaries).
@@ -411,16 +411,36 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   }
   constexpr int KROW = k_stage_row_bytes<D>();
   const int p_first = page_of(a, t_begin);
-  // Sub-page blocks: the raw page ids of the block the next load() reads,
-  // read with scalar loads one block ahead like pid_next; columns past the
-  // item's last page are clamped to it (its tokens are masked).
-  int ids_next[MODE >= kModeSubpage ? SUB_PAGES : 1];
+  // Sub-page and generic blocks: the raw page ids of the block the next
+  // load() reads, read with scalar loads one block ahead like pid_next;
+  // columns past the item's last page are clamped to it (its tokens are
+  // masked).  Generic mode (page sizes >= 3 that neither divide nor are a
+  // multiple of 16; the MFMA engine sends 1 and 2 to the sub-page mode):
+  // 16 tokens starting anywhere in a page span at most
+  // floor((ps + 14) / ps) + 1 <= 6 pages, the block's first page and its
+  // first token's slot (gen_r0) are found by an exact float-reciprocal
+  // division, and each token's page index and slot follow from
+  // pos = gen_r0 + token: (pos + 0.5) / ps is never within 0.5 / ps of an
+  // integer, so truncating its float value is exact for the small pos here.
+  constexpr int GEN_PAGES = 6;
+  int ids_next[MODE >= kModeSubpage ? SUB_PAGES : (MODE == kModeGeneric ? GEN_PAGES : 1)];
   const int p_last = t_end > t_begin ? page_of(a, t_end - 1) : p_first;
+  const float inv_ps = 1.0f / (float)a.ps;
+  int gen_r0 = 0;
   auto fetch_ids = [&](int jb) {
     if constexpr (MODE >= kModeSubpage) {
       const int p0 = p_first + jb * SUB_PAGES;
 #pragma unroll
       for (int k = 0; k < SUB_PAGES; ++k)
+        ids_next[k] = load_uniform_i32(bt_row + (int64_t)min(p0 + k, p_last) * ids_stride);
+    } else if constexpr (MODE == kModeGeneric) {
+      const int t0 = t_begin + jb * kBlockTokens;
+      int p0 = __builtin_amdgcn_readfirstlane((int)(((float)t0 + 0.5f) * inv_ps));
+      p0 -= p0 * a.ps > t0 ? 1 : 0;  // exact for t0 < 2^23
+      p0 += (p0 + 1) * a.ps <= t0 ? 1 : 0;
+      gen_r0 = t0 - p0 * a.ps;
+#pragma unroll
+      for (int k = 0; k < GEN_PAGES; ++k)
         ids_next[k] = load_uniform_i32(bt_row + (int64_t)min(p0 + k, p_last) * ids_stride);
     }
   };
@@ -466,20 +486,26 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
       }
       fetch_ids(min(jb + nw, nblk - 1));
     } else {
-      // Any page size: each token looks up its own page; tokens past the
-      // end are clamped to the last valid token (and masked in compute).
-      const int t0 = t_begin + jb * kBlockTokens;
+      // Generic page size (>= 3): token 4g+i is at pos = gen_r0 + 4g+i from
+      // the start of the block's first page, i.e. in page pos / ps of the
+      // block's (up to 6) prefetched ids, slot pos mod ps.  The ids are used
+      // up before the next block's are fetched into the same registers.
+#pragma unroll
+      for (int k = 0; k < GEN_PAGES; ++k) ids_next[k] = clamp_page(ids_next[k], a.num_pages);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int tv = min(t0 + 4 * g + i, t_end - 1);
-        const int page = page_of(a, tv);
-        const int phys = clamp_page(bt_row[(int64_t)page * ids_stride], a.num_pages);
-        const int64_t slot = tv - page * a.ps;
-        const char* kr = k_head + ((int64_t)phys * a.skp + slot * a.sks + r16 * DT) * 2;
-        const char* vr = v_head + ((int64_t)phys * a.svp + slot * a.svs + r16 * DT) * 2;
+        const int pos = gen_r0 + 4 * g + i;
+        const int idx = (int)(((float)pos + 0.5f) * inv_ps);
+        const int slot = pos - idx * a.ps;
+        int phys = ids_next[0];
+#pragma unroll
+        for (int k = 1; k < GEN_PAGES; ++k) phys = idx == k ? ids_next[k] : phys;
+        const char* kr = k_head + ((int64_t)phys * a.skp + (int64_t)slot * a.sks + r16 * DT) * 2;
+        const char* vr = v_head + ((int64_t)phys * a.svp + (int64_t)slot * a.svs + r16 * DT) * 2;
         t.k[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(kr));
         t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(vr));
       }
+      fetch_ids(min(jb + nw, nblk - 1));
     }
   };
 

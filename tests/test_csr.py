@@ -297,9 +297,11 @@ def test_oversubscribed_grid(case):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("ps", [1, 2, 4, 8])
+@pytest.mark.parametrize("ps", [1, 2, 4, 8, 3, 5, 12, 24, 48])
 def test_subpage_blocks_ragged_planned(ps):
-    """Page sizes dividing 16: each 16-token block spans 16 / page_size pages read by page id in registers.
+    """Page sizes that are not multiples of 16: a 16-token block spans several pages whose ids are read
+    ahead into registers (16 / page_size pages for page sizes dividing 16; up to 6 pages at any
+    offset for the others, 3 and up).
 
     Ragged lengths (partial last blocks and pages, an empty row, one row of a
     single token) on shuffled pages, through the planner, a static split and
