@@ -362,26 +362,65 @@ constexpr int kModeGeneric = 0;
 constexpr int kModeUniform = 1;
 constexpr int kModeSubpage = 2;
 
+// head_dim 256 keeps the Q^T operand in LDS instead of 32 VGPRs per lane
+// (with it in registers the kernel spilled 25-38 VGPRs to scratch inside
+// the streaming loop).  One padded 16-row copy per workgroup: every lane
+// writes its own fragments and reads back only those addresses, so no
+// barrier is needed (the waves write identical values).
+template <int D>
+constexpr bool q_in_lds() { return D >= 256; }
+template <int D>
+constexpr int q_stage_bytes() { return q_in_lds<D>() ? 16 * k_stage_row_bytes<D>() : 0; }
+
 template <int D, int MODE>
 __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_first, const int32_t* bt_row,
                                                int64_t ids_stride, int b, int kvh, int t_begin, int t_end,
                                                int nblk, int wave, int nw, int lane, float2* sm_ml, float* sm_o,
-                                               char* k_stage) {
+                                               char* k_stage, char* q_stage) {
   constexpr int DK = D / 32;  // 16-byte K chunks per lane per token
   constexpr int DT = D / 16;  // PV output tiles; V halves per lane per token
   constexpr int NDW = DT / 2;
+  // A lane's DT halves of a token row are NSEG segments of SEG dwords, so
+  // that the 16 lanes of a group read 16*SEG*4 contiguous bytes per load
+  // instruction: half dt is head_dim slot dim(r16, dt) =
+  // (dt / (2*SEG)) * (D / NSEG) + r16 * 2*SEG + dt % (2*SEG).  One segment
+  // (the slice r16*DT .. +DT) up to head_dim 128; head_dim 256 reads two
+  // 256-byte row halves rather than 16 strided 32-byte slices.
+  constexpr int SEG = NDW > 4 ? 4 : NDW;
+  constexpr int NSEG = NDW / SEG;
+  constexpr int SEG_HALVES = D / NSEG;  // head_dim distance between segments
+  auto load_slice = [](const char* p) -> HVec<NDW> {
+    if constexpr (NSEG == 1) {
+      return load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(p));
+    } else {
+      HVec<NDW> r;
+#pragma unroll
+      for (int sg = 0; sg < NSEG; ++sg) {
+        const HVec<SEG> x = load_hvec_stream<SEG>(reinterpret_cast<const _Float16*>(p) + sg * SEG_HALVES);
+#pragma unroll
+        for (int w = 0; w < SEG; ++w) r.w[sg * SEG + w] = x.w[w];
+      }
+      return r;
+    }
+  };
   const int g = lane >> 4;
   const int r16 = lane & 15;
   const bool row_ok = r16 < a.gqa;
   // The wave's Q^T operand (B of S^T = K.Q^T: row r16, head_dim slots
   // kp*32 + g*8 + [0,8)), loaded after the first K/V block is in flight.
-  h8_t qv[DK];
+  h8_t qv[q_in_lds<D>() ? 1 : DK];
+  auto q_slot = [&](int kp) -> h8_t* {
+    return reinterpret_cast<h8_t*>(q_stage + r16 * k_stage_row_bytes<D>() + (kp * 32 + g * 8) * 2);
+  };
   auto load_q = [&]() {
     const _Float16* qrow = a.q + (int64_t)b * a.sqb + (int64_t)(kvh * a.gqa + (row_ok ? r16 : 0)) * a.sqh;
 #pragma unroll
     for (int kp = 0; kp < DK; ++kp) {
       const h8_t x = *reinterpret_cast<const h8_t*>(qrow + kp * 32 + g * 8);
-      qv[kp] = row_ok ? x : (h8_t)0;
+      if constexpr (q_in_lds<D>())
+        *q_slot(kp) = row_ok ? x : (h8_t)0;
+      else
+        qv[kp] = row_ok ? x : (h8_t)0;
     }
   };
 
@@ -395,8 +434,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   const char* v_head = reinterpret_cast<const char*>(a.v + (int64_t)kvh * a.svh);
   // Lane byte offsets inside a 16-token slab of one page (loop invariant).
   // K and V are both read as whole token rows: lane (g, r16) reads row
-  // 4g+i, head_dim slice r16*DT, so one load instruction covers four full
-  // rows (contiguous 256 B each at head_dim 128).  K then goes through LDS
+  // 4g+i, segments at head_dim r16*2*SEG (+ D/NSEG), so one load
+  // instruction covers four rows (contiguous 256 B each at head_dim 128).  K then goes through LDS
   // into the MFMA operand layout (token per lane%16).
   // Sub-page blocks: token 4g+i sits in slot (4g+i) mod page_size of its
   // page (blocks start on page boundaries), again loop invariant.
@@ -406,8 +445,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = MODE >= kModeSubpage ? (4 * g + i) & ((1 << SUB_SHIFT) - 1) : 4 * g + i;
-    koff[i] = (uint32_t)(((int64_t)row * a.sks + r16 * DT) * 2);
-    voff[i] = (uint32_t)(((int64_t)row * a.svs + r16 * DT) * 2);
+    koff[i] = (uint32_t)(((int64_t)row * a.sks + r16 * 2 * SEG) * 2);
+    voff[i] = (uint32_t)(((int64_t)row * a.svs + r16 * 2 * SEG) * 2);
   }
   constexpr int KROW = k_stage_row_bytes<D>();
   const int p_first = page_of(a, t_begin);
@@ -463,9 +502,9 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
       const char* kb = k_head + ((int64_t)phys * a.skp + (int64_t)slot0 * a.sks) * 2;
       const char* vb = v_head + ((int64_t)phys * a.svp + (int64_t)slot0 * a.svs) * 2;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) t.k[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(kb + koff[i]));
+      for (int i = 0; i < 4; ++i) t.k[i] = load_slice(kb + koff[i]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(vb + voff[i]));
+      for (int i = 0; i < 4; ++i) t.v[i] = load_slice(vb + voff[i]);
     } else if constexpr (MODE >= kModeSubpage) {
       // page_size divides 16: the block covers SUB_PAGES whole pages whose
       // ids arrived during the previous compute(); lane group g picks the
@@ -481,8 +520,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
         const int c0 = ids_next[i >> SUB_SHIFT], c1 = ids_next[(4 + i) >> SUB_SHIFT];
         const int c2 = ids_next[(8 + i) >> SUB_SHIFT], c3 = ids_next[(12 + i) >> SUB_SHIFT];
         const int phys = g == 0 ? c0 : (g == 1 ? c1 : (g == 2 ? c2 : c3));
-        t.k[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(k_head + (int64_t)phys * kpage + koff[i]));
-        t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(v_head + (int64_t)phys * vpage + voff[i]));
+        t.k[i] = load_slice(k_head + (int64_t)phys * kpage + koff[i]);
+        t.v[i] = load_slice(v_head + (int64_t)phys * vpage + voff[i]);
       }
       fetch_ids(min(jb + nw, nblk - 1));
     } else {
@@ -500,10 +539,10 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
         int phys = ids_next[0];
 #pragma unroll
         for (int k = 1; k < GEN_PAGES; ++k) phys = idx == k ? ids_next[k] : phys;
-        const char* kr = k_head + ((int64_t)phys * a.skp + (int64_t)slot * a.sks + r16 * DT) * 2;
-        const char* vr = v_head + ((int64_t)phys * a.svp + (int64_t)slot * a.svs + r16 * DT) * 2;
-        t.k[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(kr));
-        t.v[i] = load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(vr));
+        const char* kr = k_head + ((int64_t)phys * a.skp + (int64_t)slot * a.sks + r16 * 2 * SEG) * 2;
+        const char* vr = v_head + ((int64_t)phys * a.svp + (int64_t)slot * a.svs + r16 * 2 * SEG) * 2;
+        t.k[i] = load_slice(kr);
+        t.v[i] = load_slice(vr);
       }
       fetch_ids(min(jb + nw, nblk - 1));
     }
@@ -512,28 +551,41 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   auto compute = [&](KVTile<D>& t, int jb) {
     const int t0 = t_begin + jb * kBlockTokens;
     const bool full = t0 + kBlockTokens <= t_end;
-    // K rows -> LDS (row 4g+i, slice r16*DT), then the MFMA A operand back
+    // K rows -> LDS (row 4g+i, the lane's segments), then the MFMA A operand back
     // out: lane (g, r16) takes token r16, head_dim kp*32 + g*8 + [0, 8).
     // LDS accesses of one wave complete in order, so the reads see the
     // writes, and the next block's writes follow these reads.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t* dst = reinterpret_cast<uint32_t*>(k_stage + (4 * g + i) * KROW + r16 * DT * 2);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(k_stage + (4 * g + i) * KROW + r16 * SEG * 4);
 #pragma unroll
-      for (int w = 0; w < NDW; ++w) dst[w] = t.k[i].w[w];
+      for (int w = 0; w < NDW; ++w) dst[(w / SEG) * (SEG_HALVES / 2) + w % SEG] = t.k[i].w[w];
     }
-    h8_t kk[DK];
+    // (head_dim 256 reads each A fragment just before its MFMAs.)
+    h8_t kk[q_in_lds<D>() ? 1 : DK];
+    if constexpr (!q_in_lds<D>()) {
 #pragma unroll
-    for (int kp = 0; kp < DK; ++kp)
-      kk[kp] = *reinterpret_cast<const h8_t*>(k_stage + r16 * KROW + (kp * 32 + g * 8) * 2);
+      for (int kp = 0; kp < DK; ++kp)
+        kk[kp] = *reinterpret_cast<const h8_t*>(k_stage + r16 * KROW + (kp * 32 + g * 8) * 2);
+    }
     // S^T[token 4g+i][row r16] over head_dim.
     f4_t sacc = (f4_t)0.f;
 #pragma unroll
     for (int kp = 0; kp < DK; ++kp) {
-      const h4_t k_lo = __builtin_shufflevector(kk[kp], kk[kp], 0, 1, 2, 3);
-      const h4_t k_hi = __builtin_shufflevector(kk[kp], kk[kp], 4, 5, 6, 7);
-      const h4_t q_lo = __builtin_shufflevector(qv[kp], qv[kp], 0, 1, 2, 3);
-      const h4_t q_hi = __builtin_shufflevector(qv[kp], qv[kp], 4, 5, 6, 7);
+      h8_t kf;
+      if constexpr (q_in_lds<D>())
+        kf = *reinterpret_cast<const h8_t*>(k_stage + r16 * KROW + (kp * 32 + g * 8) * 2);
+      else
+        kf = kk[kp];
+      const h4_t k_lo = __builtin_shufflevector(kf, kf, 0, 1, 2, 3);
+      const h4_t k_hi = __builtin_shufflevector(kf, kf, 4, 5, 6, 7);
+      h8_t qk;
+      if constexpr (q_in_lds<D>())
+        qk = *q_slot(kp);
+      else
+        qk = qv[kp];
+      const h4_t q_lo = __builtin_shufflevector(qk, qk, 0, 1, 2, 3);
+      const h4_t q_hi = __builtin_shufflevector(qk, qk, 4, 5, 6, 7);
       sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k_lo, q_lo, sacc, 0, 0, 0);
       sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k_hi, q_hi, sacc, 0, 0, 0);
     }
@@ -611,21 +663,24 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   // Row totals: the four 16-lane groups hold disjoint token subsets.
   float l_tot = l_run + shfl_xor_f(l_run, 16);
   l_tot += shfl_xor_f(l_tot, 32);
+  auto o_slot = [&](int i, int dt) {
+    return (dt / (2 * SEG)) * SEG_HALVES + (4 * g + i) * 2 * SEG + dt % (2 * SEG);
+  };
   if (row_ok) {
     if (g == 0) sm_ml[wave * 16 + r16] = make_float2(m_run, l_tot);
-    // Lane owns O[row r16][g*D/4 + i*DT + dt]: for each i, DT consecutive
-    // floats, written as 16- or 8-byte vectors.
-    float* dst = sm_o + (wave * a.gqa + r16) * wave_row_floats<D>() + g * (D / 4);
+    // Lane owns O[row r16][dim(4g+i, dt)]: for each i, NSEG runs of 2*SEG
+    // consecutive floats, written as 16- or 8-byte vectors.
+    float* dst = sm_o + (wave * a.gqa + r16) * wave_row_floats<D>();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (DT % 4 == 0) {
 #pragma unroll
         for (int dt = 0; dt < DT; dt += 4)
-          *reinterpret_cast<f4_t*>(dst + i * DT + dt) = f4_t{o[dt][i], o[dt + 1][i], o[dt + 2][i], o[dt + 3][i]};
+          *reinterpret_cast<f4_t*>(dst + o_slot(i, dt)) = f4_t{o[dt][i], o[dt + 1][i], o[dt + 2][i], o[dt + 3][i]};
       } else {
 #pragma unroll
         for (int dt = 0; dt < DT; dt += 2)
-          *reinterpret_cast<float2*>(dst + i * DT + dt) = make_float2(o[dt][i], o[dt + 1][i]);
+          *reinterpret_cast<float2*>(dst + o_slot(i, dt)) = make_float2(o[dt][i], o[dt + 1][i]);
       }
     }
   }
@@ -1173,7 +1228,8 @@ void pad_phase1_kernel(const Phase1Args a) {
 
   if constexpr (ENGINE == 0) {
     wave_loop_mfma<D, MODE>(a, phys_first, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw,
-                               lane, sm_ml, sm_o, k_stage_all + wave * k_stage_bytes<D>());
+                               lane, sm_ml, sm_o, k_stage_all + wave * k_stage_bytes<D>(),
+                               k_stage_all + nw * k_stage_bytes<D>());
   } else {
     wave_loop_valu<D, MODE == kModeUniform, GQA_T>(a, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw, lane,
                                       sm_ml, sm_o);
@@ -1561,7 +1617,8 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   const int nw = plan.waves_per_group;
   // Dynamic LDS: wave (m, l) [nw][16], wave O [nw][gqa][D + 4], and for the MFMA
   // engine one padded 16-row K staging tile per wave.
-  const size_t k_stage = engine == 0 ? (size_t)nw * 16 * (d->head_dim * 2 + 16) : 0;
+  // ... and, for head_dim 256, one padded 16-row copy of Q^T.
+  const size_t k_stage = engine == 0 ? (size_t)(nw + (d->head_dim >= 256 ? 1 : 0)) * 16 * (d->head_dim * 2 + 16) : 0;
   const size_t lds =
       (size_t)nw * 16 * sizeof(float2) + (size_t)nw * gqa * (d->head_dim + 4) * sizeof(float) + k_stage;
   const dim3 grid1(S, d->num_kv_heads, d->batch);

@@ -193,6 +193,19 @@ def test_head_dims(engine, d):
         _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), engine, s)
 
 
+@pytest.mark.parametrize("ps", [1, 4, 12, 32])
+def test_head_dim_256_block_modes(ps):
+    # head_dim 256 reads each token row as two 256-byte halves and stages q in
+    # LDS: cover every block mode (sub-page, generic, uniform) and a full
+    # 16-row group.
+    lens = [5, ps * 7 + 3, 333]
+    bt, n = shuffled_table(lens, ps, spare_pages=2, extra_cols=1, seed=256 + ps)
+    k, v = make_cache(n, ps, 1, 256, seed=256 + ps)
+    q = torch.randn(3, 16, 256, generator=torch.Generator().manual_seed(ps))
+    for s in (None, 1, 4):
+        _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), 0, s)
+
+
 @pytest.mark.parametrize("engine", ENGINES)
 def test_scaled_keys_stress_softmax_range(engine):
     lens = [300, 64]
