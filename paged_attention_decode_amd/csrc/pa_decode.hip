@@ -66,7 +66,12 @@ constexpr int kMinBlocks = 16;
 // Fewest blocks per split for short latency-bound sequences (split counts up
 // to 16, which one merge round trip covers).
 constexpr int kMinBlocksShort = 4;
-constexpr int kMergeLdsBudget = 48 * 1024;  // bytes of LDS for the wave merge
+// LDS of one workgroup (wave merge + MFMA staging) is capped so that the
+// widest rows (head_dim 256, 16-row groups) still get 5 waves in a
+// workgroup that fits a CU's 160 KB: one 2-wave workgroup per split left
+// those shapes latency-bound (16/1 d256 batch 8 x 8192: 35.2 against
+// 24.7 us).
+constexpr int kLdsBudget = 136 * 1024;
 // Headroom (base-2 units) a score may exceed the running reference max before
 // the accumulators are rescaled; fp16 weights stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
@@ -1329,9 +1334,18 @@ static int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 // VALU engine instantiations exist for these (head_dim, group) pairs.
 static bool valu_supported(int d, int gqa) { return (d == 64 || d == 128) && gqa <= 8; }
 
-static int merge_wave_cap(int gqa, int d) {
-  const int per_wave = 16 * 8 + gqa * (d + 4) * 4;
-  int cap = kMergeLdsBudget / per_wave;
+// Dynamic LDS of a workgroup: wave (m, l) [nw][16], wave O [nw][gqa][D + 4],
+// and for the MFMA engine one padded 16-row K staging tile per wave plus,
+// for head_dim 256, one padded 16-row copy of Q^T.
+static size_t group_lds_bytes(int nw, int gqa, int d, int engine) {
+  const size_t stage = engine == 0 ? (size_t)16 * (d * 2 + 16) : 0;
+  const size_t q_stage = (engine == 0 && d >= 256) ? stage : 0;
+  return (size_t)nw * (16 * sizeof(float2) + (size_t)gqa * (d + 4) * sizeof(float) + stage) + q_stage;
+}
+
+static int lds_wave_cap(int gqa, int d, int engine) {
+  const size_t per_wave = group_lds_bytes(1, gqa, d, engine) - group_lds_bytes(0, gqa, d, engine);
+  int cap = (int)((kLdsBudget - group_lds_bytes(0, gqa, d, engine)) / per_wave);
   if (cap > kMaxWaves) cap = kMaxWaves;
   if (cap < 1) cap = 1;
   return cap;
@@ -1445,7 +1459,7 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     S = ceil_div(max_pages, pps);
   }
   // Waves per workgroup: never more than the split has blocks or the wave
-  // merge's LDS allows.
+  // workgroup LDS budget allows.
   const int64_t split_tokens = (int64_t)pps * d->page_size;
   int nw = (int)((split_tokens + kBlockTokens - 1) / kBlockTokens);
   // Bandwidth-bound shapes run 4 waves per workgroup, except head_dim <= 64
@@ -1457,7 +1471,7 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   const bool narrow_rows = d->head_dim <= 64 && units <= num_cus;
   const int nw_max = (latency_bound || narrow_rows) ? kMaxWaves : kMaxWaves / 2;
   if (nw > nw_max) nw = nw_max;
-  const int cap = merge_wave_cap(gqa, d->head_dim);
+  const int cap = lds_wave_cap(gqa, d->head_dim, engine);
   if (nw > cap) nw = cap;
   if (nw < 1) nw = 1;
 
@@ -1615,12 +1629,7 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.nw = plan.waves_per_group;
 
   const int nw = plan.waves_per_group;
-  // Dynamic LDS: wave (m, l) [nw][16], wave O [nw][gqa][D + 4], and for the MFMA
-  // engine one padded 16-row K staging tile per wave.
-  // ... and, for head_dim 256, one padded 16-row copy of Q^T.
-  const size_t k_stage = engine == 0 ? (size_t)(nw + (d->head_dim >= 256 ? 1 : 0)) * 16 * (d->head_dim * 2 + 16) : 0;
-  const size_t lds =
-      (size_t)nw * 16 * sizeof(float2) + (size_t)nw * gqa * (d->head_dim + 4) * sizeof(float) + k_stage;
+  const size_t lds = group_lds_bytes(nw, gqa, d->head_dim, engine);
   const dim3 grid1(S, d->num_kv_heads, d->batch);
 
   if (events && events[0] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[0]), hs) != hipSuccess)

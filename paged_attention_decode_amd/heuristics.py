@@ -29,7 +29,7 @@ MAX_WAVES = 8              # waves per phase-1 workgroup (4 once the CUs are fil
 MAX_SPLITS = 1024          # PAD_MAX_SPLITS
 MIN_BLOCKS = 16            # 16-token blocks per split, at least
 MIN_BLOCKS_SHORT = 4       # the same for short latency-bound sequences (<= 16 splits)
-MERGE_LDS_BUDGET = 48 * 1024
+LDS_BUDGET = 136 * 1024    # LDS of one workgroup: wave merge + MFMA staging
 OVERSUBSCRIBE_SPLITS = 4   # items per unit on an oversubscribed grid
 PLAN_MAX_BATCH = 256       # largest batch the in-kernel planner handles
 
@@ -48,8 +48,16 @@ def _cdiv(a: int, b: int) -> int:
     return -(-a // b)
 
 
+def group_lds_bytes(nw: int, gqa: int, head_dim: int, engine: int = 0) -> int:
+    """Dynamic LDS of a workgroup: per wave (m, l) [16] and O [gqa][D + 4] in fp32, plus for the MFMA
+    engine a padded 16-row K staging tile per wave and, at head_dim 256, one padded 16-row Q^T copy."""
+    stage = 16 * (2 * head_dim + 16) if engine == 0 else 0
+    q_stage = stage if engine == 0 and head_dim >= 256 else 0
+    return nw * (16 * 8 + gqa * (head_dim + 4) * 4 + stage) + q_stage
+
+
 def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int, max_pages: int,
-         num_splits: int = 0, num_cus: int = 256) -> Plan:
+         num_splits: int = 0, num_cus: int = 256, engine: int = 0) -> Plan:
     """Same result as ``pad_decode_plan`` for valid arguments."""
     if num_cus <= 0:
         num_cus = 256
@@ -78,8 +86,9 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     nw = _cdiv(pps * page_size, BLOCK_TOKENS)
     narrow_rows = head_dim <= 64 and units <= num_cus
     nw = min(nw, MAX_WAVES if latency_bound or narrow_rows else MAX_WAVES // 2)
-    per_wave = 16 * 8 + gqa * (head_dim + 4) * 4
-    cap_w = max(min(MERGE_LDS_BUDGET // per_wave, MAX_WAVES), 1)
+    fixed = group_lds_bytes(0, gqa, head_dim, engine)
+    per_wave = group_lds_bytes(1, gqa, head_dim, engine) - fixed
+    cap_w = max(min((LDS_BUDGET - fixed) // per_wave, MAX_WAVES), 1)
     nw = max(min(nw, cap_w), 1)
     single = s == 1
     ws = 0 if single else workspace_bytes(batch, num_kv_heads, gqa, head_dim, s)

@@ -78,6 +78,11 @@ def test_status_strings():
     (512, 12, 2, 128, 16, 256, 0, 256),
     (64, 8, 4, 64, 16, 32, 0, 256),
     (64, 8, 4, 64, 16, 64, 0, 256),
+    (8, 16, 1, 256, 16, 512, 0, 256),
+    (16, 32, 2, 256, 16, 256, 0, 256),
+    (64, 24, 2, 256, 16, 128, 0, 256),
+    (1, 11, 1, 256, 16, 512, 0, 256),
+    (4, 16, 1, 128, 16, 256, 0, 256),
 ])
 def test_plan_matches_python_mirror(batch, hq, hkv, d, ps, max_pages, splits, cus):
     lib = _native.capi()
@@ -95,6 +100,18 @@ def test_plan_matches_python_mirror(batch, hq, hkv, d, ps, max_pages, splits, cu
     assert lib.pad_decode_counters_needed(ctypes.byref(_dims(batch, hq, hkv, d, ps, max_pages)), splits, cus,
                                           ctypes.byref(nc)) == 0
     assert nc.value == m.counters
+
+
+@pytest.mark.parametrize("d", [32, 64, 96, 128, 256])
+def test_planned_waves_fit_lds(d):
+    # Every group size and split shape: the planned workgroup fits a CU's
+    # 160 KB of LDS, and the widest rows still get 4+ waves.
+    for gqa in range(1, 17):
+        for batch, max_pages in ((1, 512), (8, 512), (64, 128), (256, 64)):
+            for engine in (0, 1):
+                m = heuristics.plan(batch, gqa, 1, d, 16, max_pages, 0, 256, engine)
+                assert heuristics.group_lds_bytes(m.waves_per_group, gqa, d, engine) <= 160 * 1024
+    assert heuristics.plan(8, 16, 1, 256, 16, 512).waves_per_group == 5
 
 
 def test_heuristic_properties():
