@@ -541,9 +541,17 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
         const int pos = gen_r0 + 4 * g + i;
         const int idx = (int)(((float)pos + 0.5f) * inv_ps);
         const int slot = pos - idx * a.ps;
-        int phys = ids_next[0];
-#pragma unroll
-        for (int k = 1; k < GEN_PAGES; ++k) phys = idx == k ? ids_next[k] : phys;
+        // idx in [0, 6): a binary mux over idx's bits.  (An equality select
+        // chain was folded into an indexed read of the id array, which the
+        // compiler placed in scratch memory: a vector memory round trip per
+        // token that also drained the K/V loads in flight.)
+        static_assert(GEN_PAGES == 6, "mux below covers 6 page ids");
+        const bool b0 = (idx & 1) != 0;
+        const int p01 = b0 ? ids_next[1] : ids_next[0];
+        const int p23 = b0 ? ids_next[3] : ids_next[2];
+        const int p45 = b0 ? ids_next[5] : ids_next[4];
+        const int p03 = (idx & 2) ? p23 : p01;
+        const int phys = (idx & 4) ? p45 : p03;
         const char* kr = k_head + ((int64_t)phys * a.skp + (int64_t)slot * a.sks + r16 * 2 * SEG) * 2;
         const char* vr = v_head + ((int64_t)phys * a.svp + (int64_t)slot * a.svs + r16 * 2 * SEG) * 2;
         t.k[i] = load_slice(kr);
