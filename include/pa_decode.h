@@ -36,7 +36,9 @@
  *  - `workspace` (pad_decode_workspace_bytes()): the fp32 split partials;
  *    no state is kept in it between launches;
  *  - `counters` (pad_decode_counters_needed() int32 entries): one arrival
- *    counter per (sequence, kv head).  They must be zero before the first
+ *    counter per (sequence, kv head), plus one per split slot when a
+ *    sequence may get more than 48 splits (those merge in two levels,
+ *    groups of 16 splits first).  They must be zero before the first
  *    launch that uses them (pad_decode_counters_init() or any zero-filled
  *    allocation), and every launch leaves them zero again.
  * Launches that may run at the same time must not share either buffer (give
@@ -136,7 +138,9 @@ int pad_decode_workspace_bytes(const pad_decode_dims* dims, int num_splits,
                                int num_cus, size_t* bytes);
 
 /* int32 arrival counters a launch with these arguments needs (0 when the
- * plan is single-pass; batch * num_kv_heads otherwise).  Pure host
+ * plan is single-pass; otherwise U = batch * num_kv_heads, or U * (1 +
+ * num_splits) when U * num_splits > 48, so that a sequence may get more
+ * than 48 split items and merge them in two levels).  Pure host
  * function.  No counterpart in the reference, whose two kernel launches
  * needed no arrival counting. */
 int pad_decode_counters_needed(const pad_decode_dims* dims, int num_splits,

@@ -66,6 +66,8 @@ constexpr int kMinBlocks = 16;
 // Fewest blocks per split for short latency-bound sequences (split counts up
 // to 16, which one merge round trip covers).
 constexpr int kMinBlocksShort = 4;
+// Units with more splits than this merge in two levels (groups of 16).
+constexpr int kTwoLevelSplits = 48;
 // LDS of one workgroup (wave merge + MFMA staging) is capped so that the
 // widest rows (head_dim 256, 16-row groups) still get 5 waves in a
 // workgroup that fits a CU's 160 KB: one 2-wave workgroup per split left
@@ -103,7 +105,7 @@ struct Phase1Args {
   _Float16* out;
   float* o_part;   // [G, gqa, D], one slot per workgroup of the grid
   float2* ml_part; // [G, gqa]  (m in base-2 units, l)
-  int* counters;   // [B, Hkv] arrival counts, zero between launches
+  int* counters;   // [B, Hkv] arrival counts, then per-slot group counts; zero between launches
   int64_t sqb, sqh;
   int64_t skp, sks, skh;
   int64_t svp, svs, svh;
@@ -252,23 +254,25 @@ template <int N>
 struct MergeBatch {
   float2 ml[N];
   f4_t o[N];
+  // Entry sp0 + j sits in split slot (sp0 + j) * stride.
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t o_rsrc, __amdgpu_buffer_rsrc_t ml_rsrc, int sp0,
-                                       int gqa, int row, int col, int d) {
+                                       int stride, int gqa, int row, int col, int d) {
 #pragma unroll
-    for (int j = 0; j < N; ++j) ml[j] = load_device_f2(ml_rsrc, (uint32_t)((sp0 + j) * gqa + row) * 8u);
+    for (int j = 0; j < N; ++j) ml[j] = load_device_f2(ml_rsrc, (uint32_t)((sp0 + j) * stride * gqa + row) * 8u);
 #pragma unroll
     for (int j = 0; j < N; ++j)
-      o[j] = load_device_f4(o_rsrc, ((uint32_t)((sp0 + j) * gqa + row) * (uint32_t)d + col) * 4u);
+      o[j] = load_device_f4(o_rsrc, ((uint32_t)((sp0 + j) * stride * gqa + row) * (uint32_t)d + col) * 4u);
   }
-  // Splits at or past nsplit fold with m_s = -inf, i.e. weight 0 (their
-  // loads read zeros): the fold has no branch, so the compiler cannot sink a
-  // load into a conditional step and serialise the round trips.  Split 0
-  // always exists, so m is finite before any such step and alpha stays 1.
-  __device__ __forceinline__ void fold(int sp0, int nsplit, float& m, float& l, f4_t& acc) const {
+  // Entries at or past `end` fold with m_s = -inf, i.e. weight 0 (their
+  // loads read zeros: they lie past the unit's region): the fold has no
+  // branch, so the compiler cannot sink a load into a conditional step and
+  // serialise the round trips.  The first entry always exists, so m is
+  // finite before any such step and alpha stays 1.
+  __device__ __forceinline__ void fold(int sp0, int end, float& m, float& l, f4_t& acc) const {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
       // Every published split is non-empty, so its m is finite.
-      const float ms = sp0 + j < nsplit ? ml[j].x : kNegInf;
+      const float ms = sp0 + j < end ? ml[j].x : kNegInf;
       const float m_new = fmaxf(m, ms);
       const float alpha = exp2_fast(m - m_new);  // 0 while m is -inf
       const float beta = exp2_fast(ms - m_new);
@@ -279,28 +283,30 @@ struct MergeBatch {
   }
 };
 
-// Folds the partials of splits [0, nsplit) of one element, one memory round
-// trip per batch: 4, 8 or 16 splits for split counts up to 4, 8 and 16,
-// batches of 16 beyond.
+// Folds entries [first, first + count) of one element (entry i in split
+// slot i * stride), one memory round trip per batch: 4, 8 or 16 entries for
+// counts up to 4, 8 and 16, batches of 16 beyond.  Entries a batch reads
+// past the count must lie past the unit's region (they read zeros).
 __device__ __forceinline__ void merge_partials(__amdgpu_buffer_rsrc_t o_rsrc, __amdgpu_buffer_rsrc_t ml_rsrc,
-                                               int nsplit, int gqa, int row, int col, int d, float& m, float& l,
-                                               f4_t& acc) {
-  if (nsplit <= 4) {
+                                               int first, int count, int stride, int gqa, int row, int col, int d,
+                                               float& m, float& l, f4_t& acc) {
+  const int end = first + count;
+  if (count <= 4) {
     MergeBatch<4> p;
-    p.load(o_rsrc, ml_rsrc, 0, gqa, row, col, d);
-    p.fold(0, nsplit, m, l, acc);
+    p.load(o_rsrc, ml_rsrc, first, stride, gqa, row, col, d);
+    p.fold(first, end, m, l, acc);
     return;
   }
-  if (nsplit <= 8) {
+  if (count <= 8) {
     MergeBatch<8> p;
-    p.load(o_rsrc, ml_rsrc, 0, gqa, row, col, d);
-    p.fold(0, nsplit, m, l, acc);
+    p.load(o_rsrc, ml_rsrc, first, stride, gqa, row, col, d);
+    p.fold(first, end, m, l, acc);
     return;
   }
-  for (int sp0 = 0; sp0 < nsplit; sp0 += 16) {
+  for (int sp0 = first; sp0 < end; sp0 += 16) {
     MergeBatch<16> p;
-    p.load(o_rsrc, ml_rsrc, sp0, gqa, row, col, d);
-    p.fold(sp0, nsplit, m, l, acc);
+    p.load(o_rsrc, ml_rsrc, sp0, stride, gqa, row, col, d);
+    p.fold(sp0, end, m, l, acc);
   }
 }
 
@@ -1307,13 +1313,42 @@ void pad_phase1_kernel(const Phase1Args a) {
   // (vmcnt(0) covers stores on this architecture); the last one to arrive
   // reads the partials with device-scope loads and resets the counter to
   // zero for the next launch.
+  //
+  // Past kTwoLevelSplits splits one workgroup reading every partial is the
+  // tail (256 splits of 8 rows: 1 MB, ~17 us), so the merge takes two
+  // levels: the last arrival of each group of 16 consecutive splits folds
+  // the group into the slot of its first split (nothing else reads those
+  // slots any more), publishes it like a partial and counts the group in;
+  // the last group folds the group results.
   __shared__ int s_last;
+  int* unit_counter = a.counters + (int64_t)b * a.hkv + kvh;
+  int stride = 1, count = nsplit;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(a.counters + (int64_t)b * a.hkv + kvh, 1);
-    s_last = (prev == nsplit - 1);
+  if (nsplit > kTwoLevelSplits) {
+    const int grp0 = my_split & ~15;  // first split of this group
+    const int gsize = min(16, nsplit - grp0);
+    int* group_counter = a.counters + (int64_t)a.batch * a.hkv + it.slot0 + grp0;
+    if (threadIdx.x == 0) s_last = (atomicAdd(group_counter, 1) == gsize - 1);
+    __syncthreads();
+    if (!s_last) return;
+    for (int e = threadIdx.x; e < total4; e += nw * 64) {
+      const int row = e / (D / 4);
+      const int col = (e - row * (D / 4)) * 4;
+      float m = kNegInf, l = 0.f;
+      f4_t acc = (f4_t)0.f;
+      merge_partials(o_rsrc, ml_rsrc, grp0, gsize, 1, gqa, row, col, D, m, l, acc);
+      const uint32_t r = (uint32_t)(grp0 * gqa + row);
+      store_device(o_rsrc, (r * D + col) * 4u, acc);
+      if (col == 0) store_device(ml_rsrc, r * 8u, make_float2(m, l));
+    }
+    if (threadIdx.x == 0) atomicExch(group_counter, 0);
+    stride = 16;
+    count = (nsplit + 15) >> 4;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
   }
+  if (threadIdx.x == 0) s_last = (atomicAdd(unit_counter, 1) == count - 1);
   __syncthreads();
   if (!s_last) return;
   for (int e = threadIdx.x; e < total4; e += nw * 64) {
@@ -1321,14 +1356,14 @@ void pad_phase1_kernel(const Phase1Args a) {
     const int col = (e - row * (D / 4)) * 4;
     float m = kNegInf, l = 0.f;
     f4_t acc = (f4_t)0.f;
-    merge_partials(o_rsrc, ml_rsrc, nsplit, gqa, row, col, D, m, l, acc);
+    merge_partials(o_rsrc, ml_rsrc, 0, count, stride, gqa, row, col, D, m, l, acc);
     const float inv = 1.f / l;
     h4_t hv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
     *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + col) = hv;
   }
-  if (threadIdx.x == 0) atomicExch(a.counters + (int64_t)b * a.hkv + kvh, 0);
+  if (threadIdx.x == 0) atomicExch(unit_counter, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1491,7 +1526,10 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   p->reserved = 0;
   p->counters = 0;
   p->workspace_bytes = p->single_pass ? 0 : workspace_layout(d, S, nullptr, nullptr, nullptr);
-  p->counters = p->single_pass ? 0 : (int64_t)d->batch * d->num_kv_heads;
+  // One arrival counter per unit and, where a unit may get more than
+  // kTwoLevelSplits items, one per item slot for the merge's groups.
+  const int64_t units64 = (int64_t)d->batch * d->num_kv_heads;
+  p->counters = p->single_pass ? 0 : units64 + (units64 * S > kTwoLevelSplits ? units64 * S : 0);
   return PAD_OK;
 }
 

@@ -32,6 +32,7 @@ MIN_BLOCKS_SHORT = 4       # the same for short latency-bound sequences (<= 16 s
 LDS_BUDGET = 136 * 1024    # LDS of one workgroup: wave merge + MFMA staging
 OVERSUBSCRIBE_SPLITS = 4   # items per unit on an oversubscribed grid
 PLAN_MAX_BATCH = 256       # largest batch the in-kernel planner handles
+TWO_LEVEL_SPLITS = 48      # units with more splits merge in two levels (groups of 16)
 
 
 @dataclass(frozen=True)
@@ -92,7 +93,9 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     nw = max(min(nw, cap_w), 1)
     single = s == 1
     ws = 0 if single else workspace_bytes(batch, num_kv_heads, gqa, head_dim, s)
-    return Plan(s, pps, nw, single, ws, 0 if single else batch * num_kv_heads)
+    units = batch * num_kv_heads
+    counters = 0 if single else units + (units * s if units * s > TWO_LEVEL_SPLITS else 0)
+    return Plan(s, pps, nw, single, ws, counters)
 
 
 def oversubscribed(batch: int, num_kv_heads: int, max_pages: int, latency_bound: bool, num_cus: int) -> bool:

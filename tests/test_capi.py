@@ -182,7 +182,7 @@ def _launch(lib, q, k, v, bt, sl, out, ws, dm, scale, splits, engine=None, strea
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("splits", [0, 1, 6])
+@pytest.mark.parametrize("splits", [0, 1, 6, 64])
 def test_launch_through_c_abi(splits):
     from oracle.reference import decode_fp16_protocol
 
@@ -201,7 +201,12 @@ def test_launch_through_c_abi(splits):
     nc = ctypes.c_int64()
     assert lib.pad_decode_workspace_bytes(ctypes.byref(dm), splits, 0, ctypes.byref(wsb)) == 0
     assert lib.pad_decode_counters_needed(ctypes.byref(dm), splits, 0, ctypes.byref(nc)) == 0
-    assert nc.value in (0, 8)
+    # 8 (sequence, kv head) counters, plus one per split slot where a unit
+    # may get more than 48 items (two-level merge).
+    cus = ctypes.c_int()
+    assert lib.pad_device_num_cus(ctypes.byref(cus)) == 0
+    m = heuristics.plan(4, 12, 2, 128, 16, bt.shape[1], splits, cus.value)
+    assert nc.value == m.counters and nc.value in (0, 8, 8 + 8 * m.num_splits)
     # The workspace keeps no state: fill it with garbage before every launch.
     ws = torch.empty(max(wsb.value, 1), dtype=torch.uint8, device="cuda")
     counters = torch.full((max(nc.value, 1),), 12345, dtype=torch.int32, device="cuda")

@@ -92,6 +92,46 @@ def test_split_counts_agree_tightly(engine):
         torch.testing.assert_close(other, base, rtol=2e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("group,d", [(1, 64), (2, 128), (1, 256)])
+def test_many_splits_few_rows(group, d):
+    # More than 16 splits of 1-2 rows: merges of several 16-split batches
+    # (17, 40 splits; the last batch ragged) and of two levels (150 splits).
+    lens = [3000, 1111]
+    bt, total = contiguous_table(lens, 16)
+    k, v = make_cache(total + 2, 16, 4, d, seed=900 + d)
+    q = torch.randn(2, 4 * group, d, generator=torch.Generator().manual_seed(900 + group))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    base = _run(q, k, v, bt, sl, 0, num_splits=1).float()
+    for s in (17, 40, 150):
+        out = _check(q, k, v, bt, sl, 0, s)
+        torch.testing.assert_close(out.float(), base, rtol=2e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("num_splits", [60, 100, 200])
+def test_two_level_merge(num_splits):
+    # More than 48 splits of one sequence merge in two levels: groups of 16
+    # consecutive splits first (the last group ragged), then the groups.
+    lens = [5000, 3000, 1]
+    bt, total = contiguous_table(lens, 16)
+    k, v = make_cache(total + 2, 16, 2, 128, seed=77)
+    q = torch.randn(3, 8, 128, generator=torch.Generator().manual_seed(77))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    base = _run(q, k, v, bt, sl, 0, num_splits=1).float()
+    for _ in range(2):  # the group counters come back to zero
+        out = _check(q, k, v, bt, sl, 0, num_splits)
+        torch.testing.assert_close(out.float(), base, rtol=2e-3, atol=1e-3)
+
+
+def test_two_level_merge_planned_long_row():
+    # A long single-kv-head row next to a short one: the in-kernel planner
+    # hands the long unit ~255 items, which merge in two levels.
+    lens = [131072 - 5, 16]
+    bt, total = contiguous_table(lens, 16)
+    k, v = make_cache(total + 1, 16, 1, 128, seed=78)
+    q = torch.randn(2, 8, 128, generator=torch.Generator().manual_seed(78))
+    _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), 0, None)
+
+
 @pytest.mark.parametrize("engine", ENGINES)
 def test_oversplit_more_splits_than_tokens(engine):
     k, v = make_cache(1, 16, 2, 128, seed=700)
