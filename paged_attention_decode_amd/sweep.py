@@ -71,10 +71,13 @@ def sweep(name, batch, splits, trials=9, iters=30, warmup=10):
 
 # (batch, q heads, kv heads, head_dim, page_size, seq_len) of the survey.
 SURVEY_CASES = (
-    [(32, 12, 2, 128, ps, 4096) for ps in (16, 32, 8, 4, 2, 1, 12)]
+    [(32, 12, 2, 128, ps, 4096) for ps in (16, 32, 8, 4, 2, 1, 12, 3)] + [(64, 12, 2, 128, 24, 4096)]
     + [(32, 32, 8, 128, 16, 2048), (8, 32, 32, 128, 16, 4096), (32, 64, 8, 128, 16, 2048),
        (64, 16, 2, 64, 16, 4096), (32, 32, 8, 64, 16, 2048), (32, 24, 8, 96, 16, 2048),
-       (8, 32, 32, 96, 16, 4096), (32, 16, 4, 32, 16, 4096), (32, 16, 4, 256, 16, 2048)]
+       (8, 32, 32, 96, 16, 4096), (32, 16, 4, 32, 16, 4096), (32, 16, 4, 256, 16, 2048),
+       (64, 32, 8, 256, 16, 2048), (8, 16, 1, 256, 16, 8192)]
+    # long single-kv-head (MQA) rows: hundreds of splits, two-level merge
+    + [(1, 8, 1, 128, 16, 131072), (1, 16, 1, 128, 16, 262144)]
 )
 
 
