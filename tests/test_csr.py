@@ -130,6 +130,15 @@ def test_csr_ragged_batch():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("num_splits", [None, 100])
+def test_csr_two_level_merge(num_splits):
+    # A long single-kv-head row read through the CSR index: the planner (or
+    # 100 explicit splits) gives it more than 48 items, merged in two levels.
+    q, k, v, bt, sl = _primary_case([40000, 33, 1], hkv=1, group=8, seed=61)
+    _check_csr(q, k, v, bt, sl, 16, num_splits=num_splits)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("ps", [1, 8, 16, 32])
 def test_csr_shared_and_reordered_pages(ps):
     """CSR rows may share physical pages and list them in any order."""

@@ -338,20 +338,22 @@ def test_concurrent_streams_keep_their_own_scratch():
             assert torch.equal(o, outs[i][0])
 
 
-def test_graph_capture_replays():
+@pytest.mark.parametrize("case", ["ragged", "two_level"])
+def test_graph_capture_replays(case):
     # Serving engines capture the decode in a HIP graph and replay it with
     # new inputs written in place.  The launch allocates nothing once its
-    # stream's scratch exists, the split merge leaves its arrival counters at
-    # zero, and the workspace carries no state, so every replay must equal an
-    # eager call on the same inputs - with eager decodes (other scratch) run
-    # between the replays.
+    # stream's scratch exists, the split merge leaves its arrival (and group)
+    # counters at zero, and the workspace carries no state, so every replay
+    # must equal an eager call on the same inputs - with eager decodes (other
+    # scratch) run between the replays.  "two_level": a long single-kv-head
+    # row whose ~250 planned items merge in two levels.
     import paged_attention_decode_amd as pad
 
-    lens = [4096, 300, 2500, 1]
+    lens, hq, hkv = ([4096, 300, 2500, 1], 12, 2) if case == "ragged" else ([60000, 16], 8, 1)
     bt, n = shuffled_table(lens, 16, spare_pages=1, extra_cols=1, seed=91)
-    k, v = make_cache(n, 16, 2, 128, seed=91)
+    k, v = make_cache(n, 16, hkv, 128, seed=91)
     dev = [k.half().cuda(), v.half().cuda(), bt.cuda(), torch.tensor(lens, dtype=torch.int32).cuda()]
-    qs = [torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(92 + i)).half().cuda()
+    qs = [torch.randn(len(lens), hq, 128, generator=torch.Generator().manual_seed(92 + i)).half().cuda()
           for i in range(4)]
     q_static = qs[0].clone()
     s = torch.cuda.Stream()
