@@ -20,18 +20,18 @@
 //    [s*pages_per_split, (s+1)*pages_per_split), so each page and each
 //    block_table entry is read by exactly one workgroup.  The reference
 //    split by tokens (cuda/kernel_v4_split_k.cu:73-75).
-//  * A phase-1 workgroup is 1-4 wave64s; each wave walks 16-token blocks of
+//  * A phase-1 workgroup is 1-8 wave64s; each wave walks 16-token blocks of
 //    its split and keeps its own online-softmax state; the waves' states are
 //    merged through LDS at the end (one fp32 partial per workgroup).
 //  * Engine 0 (MFMA): scores are computed transposed, S^T = K . Q^T, with
 //    v_mfma_f32_16x16x16_f16 (16 tokens x 16 padded GQA rows, K = head_dim),
 //    and the output as O^T = V^T . P^T.  With S^T every lane already holds
 //    P^T in the B-operand layout of the PV product, so P never moves between
-//    lanes.  The head_dim index inside each MFMA tile is permuted so that
-//    every lane's K and V operands are 16-byte loads straight from HBM:
-//    K rows are read 64 contiguous bytes per token per instruction and V
-//    rows 256 contiguous bytes per token per instruction.  One K/V tile is
-//    shared by the whole GQA group through the MFMA B operand.
+//    lanes.  K and V are read as whole token rows (16 lanes cover a row
+//    with 16-byte loads); the head_dim index inside each PV tile is
+//    permuted so that these V registers are the MFMA A operand as loaded,
+//    and K goes through a padded LDS tile into the A layout of S^T.  One
+//    K/V tile is shared by the whole GQA group through the B operand.
 //  * Engine 1 (VALU): 16 lanes per token, fp16x2 dot products
 //    (v_dot2_f32_f16) reduced across the 16 lanes with 4 DPP steps, fp32
 //    online softmax and FMA accumulation of P.V.  Kept for the measured
@@ -39,9 +39,9 @@
 //  * Phase 2 is fused into the same launch: every workgroup of a split
 //    sequence publishes its fp32 partial with device-scope stores and counts
 //    itself in with an atomic; the last one to arrive folds all partials of
-//    its (sequence, kv head) into the fp16 output and resets the counter.  A
-//    sequence held by one split is normalised directly.  One kernel launch
-//    per call.
+//    its (sequence, kv head) into the fp16 output and resets the counter
+//    (past 48 splits in two levels, groups of 16 splits first).  A sequence
+//    held by one split is normalised directly.  One kernel launch per call.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
