@@ -1332,6 +1332,10 @@ void pad_phase1_kernel(const Phase1Args a) {
     if (threadIdx.x == 0) s_last = (atomicAdd(group_counter, 1) == gsize - 1);
     __syncthreads();
     if (!s_last) return;
+    // Each element's O is read and then overwritten by its own thread, but
+    // a row's (m, l) is read by every thread of the row, and a row can span
+    // waves and loop passes (head_dim 96: 24 elements per row): the group's
+    // (m, l) goes to LDS first and to the slot only after a barrier.
     for (int e = threadIdx.x; e < total4; e += nw * 64) {
       const int row = e / (D / 4);
       const int col = (e - row * (D / 4)) * 4;
@@ -1340,8 +1344,10 @@ void pad_phase1_kernel(const Phase1Args a) {
       merge_partials(o_rsrc, ml_rsrc, grp0, gsize, 1, gqa, row, col, D, m, l, acc);
       const uint32_t r = (uint32_t)(grp0 * gqa + row);
       store_device(o_rsrc, (r * D + col) * 4u, acc);
-      if (col == 0) store_device(ml_rsrc, r * 8u, make_float2(m, l));
+      if (col == 0) sm_ml[row] = make_float2(m, l);
     }
+    __syncthreads();
+    if (threadIdx.x < gqa) store_device(ml_rsrc, (uint32_t)(grp0 * gqa + threadIdx.x) * 8u, sm_ml[threadIdx.x]);
     if (threadIdx.x == 0) atomicExch(group_counter, 0);
     stride = 16;
     count = (nsplit + 15) >> 4;

@@ -122,6 +122,18 @@ def test_two_level_merge(num_splits):
         torch.testing.assert_close(out.float(), base, rtol=2e-3, atol=1e-3)
 
 
+def test_two_level_merge_rows_across_waves():
+    # head_dim 96 has 24 four-column elements per row, so with one wave a
+    # row's elements span two loop passes: the group merger must not publish
+    # a row's (m, l) before every pass has read the original.  (Regression:
+    # the last 8 elements of row 2 came out wrong before.)
+    lens = [153, 250, 200]
+    bt, total = contiguous_table(lens, 1)
+    k, v = make_cache(total + 2, 1, 1, 96, seed=1042)
+    q = torch.randn(3, 3, 96, generator=torch.Generator().manual_seed(1043))
+    _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), 0, 60)
+
+
 def test_two_level_merge_planned_long_row():
     # A long single-kv-head row next to a short one: the in-kernel planner
     # hands the long unit ~255 items, which merge in two levels.
@@ -433,3 +445,16 @@ def test_fuzz_shape_matrix(engine, seed):
         pytest.skip("shape outside the VALU engine")
     for s in (None, 4):
         _check(q, k, v, bt, sl, engine, s)
+
+
+@pytest.mark.parametrize("seed", range(FUZZ))
+def test_fuzz_wide_matrix(seed):
+    # MFMA engine over every head_dim, group sizes up to 16 and every block
+    # mode (sub-page 1/2/4/8, uniform 16/32, generic 3/12/24), with the
+    # heuristic plan, a fixed split and 60 splits (two-level merge once a
+    # row has more than 48 pages).
+    q, k, v, bt, sl = random_case(1000 + seed, kv_heads=(1, 2, 4), gqa=(1, 3, 8, 16),
+                                  head_dims=(32, 64, 96, 128, 256),
+                                  page_sizes=(1, 2, 3, 4, 8, 12, 16, 24, 32), min_len=0, max_len=400)
+    for s in (None, 4, 60):
+        _check(q, k, v, bt, sl, 0, s)
