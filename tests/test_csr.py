@@ -22,7 +22,7 @@ import torch
 
 from oracle.csr import csr_to_dense, paged_kv_indices as ref_indices
 from oracle.reference import decode_fp16_protocol
-from tests.helpers import assert_parity, cdiv, contiguous_table, make_cache, shuffled_table
+from tests.helpers import assert_parity, cdiv, contiguous_table, make_cache, random_case, shuffled_table
 
 
 # ---------------------------------------------------------------- CPU pins
@@ -347,3 +347,16 @@ def test_head_pair_placement(d, case):
     assert_parity(out, expected)
     for _ in range(3):
         assert torch.equal(_run_dense(q, k, v, bt, sl, num_splits=splits), out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(int(__import__("os").environ.get("PAD_KERNEL_FUZZ_ITERS", "20"))))
+def test_csr_fuzz_wide(seed):
+    # The CSR entry over random ragged batches (empty rows included), every
+    # block mode and head_dim, heuristic and explicit split counts.
+    q, k, v, bt, sl = random_case(5000 + seed, kv_heads=(1, 2, 4), gqa=(1, 2, 5, 8, 16),
+                                  head_dims=(32, 64, 96, 128, 256),
+                                  page_sizes=(1, 2, 3, 4, 8, 12, 16, 24, 32), max_batch=6, min_len=0, max_len=700)
+    ps = k.shape[1]
+    for s in (None, 7, 100):
+        _check_csr(q, k, v, bt, sl, ps, num_splits=s)

@@ -458,3 +458,22 @@ def test_fuzz_wide_matrix(seed):
                                   page_sizes=(1, 2, 3, 4, 8, 12, 16, 24, 32), min_len=0, max_len=400)
     for s in (None, 4, 60):
         _check(q, k, v, bt, sl, 0, s)
+
+
+@pytest.mark.parametrize("seed", range(max(FUZZ // 4, 1)))
+def test_fuzz_large_batches(seed):
+    # Batches of 40-300 ragged rows (empty ones included) with the heuristic
+    # plan: the in-kernel planner for up to 256 rows (an oversubscribed grid
+    # once there are at least as many (row, kv head) units as CUs), the static
+    # split beyond.
+    rng = random.Random(7000 + seed)
+    batch = rng.randint(40, 300)
+    hkv = rng.choice((2, 4, 8))
+    group = rng.choice((1, 4, 8))
+    d = rng.choice((64, 128))
+    ps = rng.choice((1, 12, 16))
+    lens = [rng.randint(0, 600) for _ in range(batch)]
+    bt, n = shuffled_table(lens, ps, spare_pages=2, extra_cols=rng.randint(0, 3), seed=7100 + seed)
+    k, v = make_cache(n, ps, hkv, d, seed=7200 + seed)
+    q = torch.randn(batch, hkv * group, d, generator=torch.Generator().manual_seed(7300 + seed))
+    _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), 0, None)
