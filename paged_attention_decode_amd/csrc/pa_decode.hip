@@ -380,8 +380,6 @@ constexpr int kModeSubpage = 2;
 // barrier is needed (the waves write identical values).
 template <int D>
 constexpr bool q_in_lds() { return D >= 256; }
-template <int D>
-constexpr int q_stage_bytes() { return q_in_lds<D>() ? 16 * k_stage_row_bytes<D>() : 0; }
 
 template <int D, int MODE>
 __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_first, const int32_t* bt_row,
@@ -580,24 +578,16 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
 #pragma unroll
       for (int w = 0; w < NDW; ++w) dst[(w / SEG) * (SEG_HALVES / 2) + w % SEG] = t.k[i].w[w];
     }
-    // (head_dim 256 reads each A fragment just before its MFMAs.)
-    h8_t kk[q_in_lds<D>() ? 1 : DK];
-    if constexpr (!q_in_lds<D>()) {
+    h8_t kk[DK];
 #pragma unroll
-      for (int kp = 0; kp < DK; ++kp)
-        kk[kp] = *reinterpret_cast<const h8_t*>(k_stage + r16 * KROW + (kp * 32 + g * 8) * 2);
-    }
+    for (int kp = 0; kp < DK; ++kp)
+      kk[kp] = *reinterpret_cast<const h8_t*>(k_stage + r16 * KROW + (kp * 32 + g * 8) * 2);
     // S^T[token 4g+i][row r16] over head_dim.
     f4_t sacc = (f4_t)0.f;
 #pragma unroll
     for (int kp = 0; kp < DK; ++kp) {
-      h8_t kf;
-      if constexpr (q_in_lds<D>())
-        kf = *reinterpret_cast<const h8_t*>(k_stage + r16 * KROW + (kp * 32 + g * 8) * 2);
-      else
-        kf = kk[kp];
-      const h4_t k_lo = __builtin_shufflevector(kf, kf, 0, 1, 2, 3);
-      const h4_t k_hi = __builtin_shufflevector(kf, kf, 4, 5, 6, 7);
+      const h4_t k_lo = __builtin_shufflevector(kk[kp], kk[kp], 0, 1, 2, 3);
+      const h4_t k_hi = __builtin_shufflevector(kk[kp], kk[kp], 4, 5, 6, 7);
       h8_t qk;
       if constexpr (q_in_lds<D>())
         qk = *q_slot(kp);
