@@ -2,6 +2,9 @@
 
     python -m paged_attention_decode_amd.profile_run --config C2 --batch 64 --calls 50
 
+``--shape B/HQ/HKV/D/L[/PS]`` replaces the configuration by B sequences of L
+tokens (page size PS, default 16) with HQ / HKV heads of head_dim D.
+
 Runs a calibration copy first (``--copy-mb`` MiB read and written by
 PyTorch's copy kernel, 3 dispatches: the bytes a FETCH_SIZE / WRITE_SIZE
 counter should report for a plain stream of known size), then ``--calls``
@@ -30,6 +33,7 @@ def main() -> None:
     p.add_argument("--num-splits", type=int, default=0)
     p.add_argument("--copy-mb", type=int, default=256)
     p.add_argument("--warm", action="store_true")
+    p.add_argument("--shape", default="", help="B/HQ/HKV/D/L[/PS]: uniform lengths instead of --config")
     a = p.parse_args()
 
     if a.copy_mb > 0:
@@ -43,9 +47,19 @@ def main() -> None:
         print(f"calibration copy: {a.copy_mb} MiB read + {a.copy_mb} MiB written per dispatch", flush=True)
         del src, dst
 
-    w0 = wl.make(a.config, batch=a.batch, seed=1)
+    if a.shape:
+        f = [int(x) for x in a.shape.split("/")]
+        b, hq, hkv, d, seq = f[:5]
+        ps = f[5] if len(f) > 5 else 16
+
+        def make(seed):
+            return wl._build(f"shape {a.shape}", [seq] * b, hq, hkv, d, ps, seed, "cuda")
+    else:
+        def make(seed):
+            return wl.make(a.config, batch=a.batch, seed=seed)
+    w0 = make(1)
     n_sets = 1 if a.warm else max(2, math.ceil(512 * (1 << 20) / (w0.k_cache.numel() * 4)) + 1)
-    sets = [w0] + [wl.make(a.config, batch=a.batch, seed=1 + i) for i in range(1, n_sets)]
+    sets = [w0] + [make(1 + i) for i in range(1, n_sets)]
     torch.cuda.synchronize()
     for i in range(a.calls):
         w = sets[i % n_sets]
