@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PAD_ABI_VERSION 2
+#define PAD_ABI_VERSION 3
 
 /* Largest supported GQA group (query heads per KV head); the reference's
  * bound is the same (cuda/kernel_v4_split_k.cu:44). */
@@ -89,7 +89,10 @@ typedef struct pad_decode_dims {
   int32_t head_dim;
   int32_t page_size;
   int32_t max_pages;        /* block_table.shape[1]                        */
-  int64_t num_pages;        /* k_cache.shape[0]; not read on the device    */
+  int64_t num_pages;        /* k_cache.shape[0]; page ids outside
+                               [0, num_pages) read page 0 instead of
+                               faulting, so a launch that reads pages
+                               needs it > 0 (else PAD_ERR_INVALID_SHAPE)   */
   int64_t q_stride[3];      /* [batch, head, dim]                          */
   int64_t k_stride[4];      /* [page, slot, kv_head, dim]                  */
   int64_t v_stride[4];
@@ -129,6 +132,19 @@ typedef struct pad_decode_plan_t {
  * full capacity, equal page chunks when the lengths are ragged. */
 int pad_decode_plan(const pad_decode_dims* dims, int num_splits, int num_cus,
                     pad_decode_plan_t* plan);
+
+/* pad_decode_plan() for pad_decode_launch_csr(): dims->max_pages is the
+ * number of entries of the CSR `indices` array (every sequence's pages), so
+ * the plan assumes max_pages / batch pages per sequence (exact when the
+ * lengths are equal; ragged batches are re-planned in-kernel from indptr
+ * under the heuristic).  An explicit num_splits cuts each sequence's own
+ * pages into that many ranges.  The workspace and counters this plan
+ * reports never exceed those of pad_decode_plan() on the same dims, so
+ * either sizes the scratch of a CSR launch.  Pure host function.  No
+ * counterpart in the reference (its FlashInfer adapter planned inside the
+ * library, src/flashinfer_adapter.py:100-112). */
+int pad_decode_plan_csr(const pad_decode_dims* dims, int num_splits,
+                        int num_cus, pad_decode_plan_t* plan);
 
 /* Bytes of workspace pad_decode_launch() needs for these arguments
  * (0 when the plan is single-pass).  Pure host function.  The reference

@@ -9,6 +9,9 @@
   ``pad_decode_plan_t``.
 * ``probe()`` - ``libpa_probe.so``, the bandwidth probes used by
   ``roofline.py`` (measurement tooling, not the decode path).
+* ``timeline()`` - ``libpa_decode_tl.so``, the decode library built with
+  per-workgroup phase stamps (include/pa_decode_timeline.h), for
+  ``profile_run --timeline`` (measurement tooling, not the decode path).
 
 Both raise ImportError with the build command when the library is missing;
 nothing here computes attention on the CPU.
@@ -84,6 +87,8 @@ class PadPlan(ctypes.Structure):
 _VP = ctypes.c_void_p
 SIGNATURES = {
     "pad_decode_plan": ([ctypes.POINTER(PadDims), ctypes.c_int, ctypes.c_int, ctypes.POINTER(PadPlan)], ctypes.c_int),
+    "pad_decode_plan_csr": (
+        [ctypes.POINTER(PadDims), ctypes.c_int, ctypes.c_int, ctypes.POINTER(PadPlan)], ctypes.c_int),
     "pad_decode_workspace_bytes": (
         [ctypes.POINTER(PadDims), ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)],
         ctypes.c_int,
@@ -127,6 +132,33 @@ def capi():
             fn.restype = restype
         _capi = lib
     return _capi
+
+
+TIMELINE_PATH = os.path.join(_PKG_DIR, "libpa_decode_tl.so")
+TIMELINE_SIGNATURES = {
+    "pad_timeline_read": ([_VP, ctypes.c_size_t], ctypes.c_int),
+    "pad_timeline_reset": ([], ctypes.c_int),
+}
+# include/pa_decode_timeline.h
+TL_LAUNCHES, TL_MAX_GROUPS, TL_SLOTS = 4, 16384, 8
+TL_ENTRY, TL_ITEM, TL_LOOP_END, TL_PUBLISHED, TL_ARRIVED, TL_MERGED, TL_EXIT, TL_INFO = range(8)
+TL_F_NO_ITEM, TL_F_SINGLE, TL_F_MERGER, TL_F_GROUP = 1, 2, 4, 8
+_timeline = None
+
+
+def timeline():
+    """ctypes handle to libpa_decode_tl.so: every decode entry point plus the stamp buffer readers."""
+    global _timeline
+    if _timeline is None:
+        if not os.path.exists(TIMELINE_PATH):
+            raise ImportError(f"paged_attention_decode_amd: {TIMELINE_PATH} is missing; {_BUILD_HINT}")
+        lib = ctypes.CDLL(TIMELINE_PATH)
+        for name, (argtypes, restype) in {**SIGNATURES, **TIMELINE_SIGNATURES}.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        _timeline = lib
+    return _timeline
 
 
 PROBE_PATH = os.path.join(_PKG_DIR, "libpa_probe.so")

@@ -1,6 +1,6 @@
 """Build the native parts of the package in-tree.
 
-Three shared libraries, all written next to this file:
+Four shared libraries, all written next to this file:
 
 * ``libpa_decode.so`` - the C-ABI library (``include/pa_decode.h``): gfx950
   kernels plus ``extern "C"`` entry points, compiled by ``hipcc`` from
@@ -11,9 +11,14 @@ Three shared libraries, all written next to this file:
   ``$ORIGIN`` rpath.
 * ``libpa_probe.so`` - bandwidth probes for the roofline report
   (``csrc/pa_probe.hip``, ``roofline.py``); not on the decode path.
+* ``libpa_decode_tl.so`` - the same source as ``libpa_decode.so`` compiled
+  with ``-DPAD_TIMELINE``: every workgroup stamps the phases of its path
+  (``include/pa_decode_timeline.h``) for ``profile_run --timeline``.
+  Measurement only; the decode path never loads it.
 
 Usage: ``python -m paged_attention_decode_amd.build`` (or ``build()`` from
-``__graft_entry__``).  Every call recompiles.
+``__graft_entry__``).  Every call recompiles; the three hipcc builds run in
+parallel.
 """
 
 from __future__ import annotations
@@ -23,6 +28,7 @@ import shlex
 import subprocess
 import sys
 import sysconfig
+from concurrent.futures import ThreadPoolExecutor
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
@@ -33,6 +39,7 @@ ARCH = "gfx950"
 
 CAPI_LIB = os.path.join(PKG_DIR, "libpa_decode.so")
 PROBE_LIB = os.path.join(PKG_DIR, "libpa_probe.so")
+TIMELINE_LIB = os.path.join(PKG_DIR, "libpa_decode_tl.so")
 EXT_NAME = "_pa_decode_ext"
 EXT_LIB = os.path.join(PKG_DIR, EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
 
@@ -68,6 +75,15 @@ def build_capi() -> str:
     _run([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", os.path.join(CSRC, "pa_decode.hip"), "-o", tmp])
     os.replace(tmp, CAPI_LIB)
     return CAPI_LIB
+
+
+def build_timeline() -> str:
+    """libpa_decode_tl.so: the decode library with per-workgroup phase stamps (measurement only)."""
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    tmp = TIMELINE_LIB + ".tmp"
+    _run([hipcc, *HIP_FLAGS, "-DPAD_TIMELINE", f"-I{INCLUDE}", os.path.join(CSRC, "pa_decode.hip"), "-o", tmp])
+    os.replace(tmp, TIMELINE_LIB)
+    return TIMELINE_LIB
 
 
 def build_probe() -> str:
@@ -123,7 +139,11 @@ def build_torch_ext() -> str:
 
 
 def build_all() -> list[str]:
-    return [build_capi(), build_torch_ext(), build_probe()]
+    with ThreadPoolExecutor(max_workers=3) as pool:
+        hip = [pool.submit(build_capi), pool.submit(build_timeline), pool.submit(build_probe)]
+        capi = hip[0].result()
+        ext = build_torch_ext()  # links against libpa_decode.so
+        return [capi, ext, hip[1].result(), hip[2].result()]
 
 
 if __name__ == "__main__":

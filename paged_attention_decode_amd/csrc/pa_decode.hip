@@ -48,8 +48,32 @@
 #include <string.h>
 
 #include "pa_decode.h"
+#include "pa_decode_timeline.h"  // slot constants; its functions exist only with -DPAD_TIMELINE
 
 namespace pad {
+
+#ifdef PAD_TIMELINE
+// Phase timeline, compiled only into the measurement library
+// (libpa_decode_tl.so, -DPAD_TIMELINE): thread 0 of every workgroup stores
+// s_memrealtime stamps (100 MHz) at fixed points of its path, for the last
+// PAD_TL_LAUNCHES launches (a ring indexed by a host-side launch count).
+// Slot meanings are the PAD_TL_* constants of pa_decode_timeline.h.
+__device__ unsigned long long tl_buf[PAD_TL_LAUNCHES * PAD_TL_MAX_GROUPS * PAD_TL_SLOTS];
+static int tl_launches = 0;
+#define PAD_TL_AT(lin, slot, value)                                                                      \
+  do {                                                                                                   \
+    if (threadIdx.x == 0 && (lin) < PAD_TL_MAX_GROUPS)                                                   \
+      ::pad::tl_buf[((size_t)a.tl_launch * PAD_TL_MAX_GROUPS + (lin)) * PAD_TL_SLOTS + (slot)] = (value); \
+  } while (0)
+#define PAD_TL(lin, slot) PAD_TL_AT(lin, slot, __builtin_amdgcn_s_memrealtime())
+#else
+#define PAD_TL_AT(lin, slot, value) \
+  do {                              \
+  } while (0)
+#define PAD_TL(lin, slot) \
+  do {                    \
+  } while (0)
+#endif
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
@@ -111,6 +135,9 @@ struct Phase1Args {
   int64_t svp, svs, svh;
   int64_t sob, soh;
   int64_t num_pages;
+#ifdef PAD_TIMELINE
+  int tl_launch;   // ring slot of this launch's stamps
+#endif
 };
 
 // Token -> page index, and pages covering n tokens (shift for power-of-two
@@ -1079,16 +1106,19 @@ __device__ WorkItem plan_item(const Phase1Args& a, const SeqTable<NK>& t, int g,
 }
 
 // The static item of workgroup (s, kvh, b) given the sequence's length and
-// page count.
+// page count.  The dense table splits every row's max_pages columns into
+// num_splits ranges of pps pages; a CSR index has no common row width, so
+// each sequence's own pages are cut into num_splits ranges.
 __device__ __forceinline__ WorkItem static_item(const Phase1Args& a, int s, int kvh, int b, int L, int pages,
                                                 const int32_t* ids_row, int64_t ids_stride) {
   WorkItem w;
+  const int pps = a.csr ? max((pages + a.num_splits - 1) / a.num_splits, 1) : a.pps;
   w.b = b;
   w.kvh = kvh;
   w.L = L;
-  w.p_begin = s * a.pps;
-  w.p_end = min(w.p_begin + a.pps, pages);
-  w.nsplit = (pages + a.pps - 1) / a.pps;
+  w.p_begin = s * pps;
+  w.p_end = min(w.p_begin + pps, pages);
+  w.nsplit = (pages + pps - 1) / pps;
   w.slot0 = (b * a.hkv + kvh) * a.num_splits;
   w.col_max = a.csr ? pages - 1 : a.max_pages - 1;
   // Splits past the sequence's last page do nothing, except split 0 of an
@@ -1174,6 +1204,16 @@ __device__ __forceinline__ void grid_pos(const Phase1Args& a, int& s, int& h, in
 template <int D, int MODE, int ENGINE, int GQA_T>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE))))
 void pad_phase1_kernel(const Phase1Args a) {
+#ifdef PAD_TIMELINE
+  const unsigned long long tl_entry = __builtin_amdgcn_s_memrealtime();
+  const unsigned long long tl_xcc = (unsigned long long)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15) << 32;
+#define PAD_TL_NOTE(item_slot, flags) \
+  PAD_TL_AT(lin, PAD_TL_INFO, (unsigned long long)(uint32_t)(item_slot) | tl_xcc | ((unsigned long long)(flags) << 40))
+#else
+#define PAD_TL_NOTE(item_slot, flags) \
+  do {                                \
+  } while (0)
+#endif
   extern __shared__ float4 smem_f4[];
   float2* sm_ml = reinterpret_cast<float2*>(smem_f4);  // [nw][16]
   const int nw = a.nw;
@@ -1183,6 +1223,7 @@ void pad_phase1_kernel(const Phase1Args a) {
 
   int s, h, bz, lin;
   grid_pos(a, s, h, bz, lin);
+  PAD_TL_AT(blockIdx.x + a.num_splits * (blockIdx.y + a.hkv * blockIdx.z), PAD_TL_ENTRY, tl_entry);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = s + a.num_splits * (h + a.hkv * bz);
@@ -1213,7 +1254,12 @@ void pad_phase1_kernel(const Phase1Args a) {
     const int L = max(static_len, 0);
     it = static_item(a, s, h, bz, L, min(pages_for(a, L), a.max_pages), static_row, a.sbp);
   }
-  if (!it.valid) return;
+  PAD_TL(lin, PAD_TL_ITEM);
+  if (!it.valid) {
+    PAD_TL_NOTE(-1, PAD_TL_F_NO_ITEM);
+    PAD_TL(lin, PAD_TL_EXIT);
+    return;
+  }
   const int b = it.b;
   const int kvh = it.kvh;
   const int nsplit = it.nsplit;
@@ -1225,6 +1271,8 @@ void pad_phase1_kernel(const Phase1Args a) {
       const int row = e / (D / 4);
       *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + (e - row * (D / 4)) * 4) = (h4_t)0;
     }
+    PAD_TL_NOTE(g, PAD_TL_F_SINGLE);
+    PAD_TL(lin, PAD_TL_EXIT);
     return;
   }
   if constexpr (ENGINE == 0 && MODE == kModeUniform) {
@@ -1244,6 +1292,7 @@ void pad_phase1_kernel(const Phase1Args a) {
                                       sm_ml, sm_o);
   }
   __syncthreads();
+  PAD_TL(lin, PAD_TL_LOOP_END);
 
   // Merge the waves' states: threads over (row, 4 consecutive d).  With a
   // single split the result is final; otherwise it is this split's partial.
@@ -1295,7 +1344,12 @@ void pad_phase1_kernel(const Phase1Args a) {
       if (col == 0) store_device(ml_rsrc, r * 8u, make_float2(M, Ls));
     }
   }
-  if (nsplit == 1) return;
+  if (nsplit == 1) {
+    PAD_TL(lin, PAD_TL_PUBLISHED);
+    PAD_TL_NOTE(g, PAD_TL_F_SINGLE);
+    PAD_TL(lin, PAD_TL_EXIT);
+    return;
+  }
 
   // Split-K merge, fused: the last workgroup of this (sequence, kv head) to
   // arrive folds every split's partial into the output.  A workgroup counts
@@ -1315,13 +1369,22 @@ void pad_phase1_kernel(const Phase1Args a) {
   int stride = 1, count = nsplit;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  PAD_TL(lin, PAD_TL_PUBLISHED);
+  int tl_flags = 0;
+  (void)tl_flags;
   if (nsplit > kTwoLevelSplits) {
     const int grp0 = my_split & ~15;  // first split of this group
     const int gsize = min(16, nsplit - grp0);
     int* group_counter = a.counters + (int64_t)a.batch * a.hkv + it.slot0 + grp0;
     if (threadIdx.x == 0) s_last = (atomicAdd(group_counter, 1) == gsize - 1);
     __syncthreads();
-    if (!s_last) return;
+    if (!s_last) {
+      PAD_TL(lin, PAD_TL_ARRIVED);
+      PAD_TL_NOTE(g, 0);
+      PAD_TL(lin, PAD_TL_EXIT);
+      return;
+    }
+    tl_flags = PAD_TL_F_GROUP;
     // Each element's O is read and then overwritten by its own thread, but
     // a row's (m, l) is read by every thread of the row, and a row can span
     // waves and loop passes (head_dim 96: 24 elements per row): the group's
@@ -1346,7 +1409,12 @@ void pad_phase1_kernel(const Phase1Args a) {
   }
   if (threadIdx.x == 0) s_last = (atomicAdd(unit_counter, 1) == count - 1);
   __syncthreads();
-  if (!s_last) return;
+  PAD_TL(lin, PAD_TL_ARRIVED);
+  if (!s_last) {
+    PAD_TL_NOTE(g, tl_flags);
+    PAD_TL(lin, PAD_TL_EXIT);
+    return;
+  }
   for (int e = threadIdx.x; e < total4; e += nw * 64) {
     const int row = e / (D / 4);
     const int col = (e - row * (D / 4)) * 4;
@@ -1360,6 +1428,10 @@ void pad_phase1_kernel(const Phase1Args a) {
     *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + col) = hv;
   }
   if (threadIdx.x == 0) atomicExch(unit_counter, 0);
+  PAD_TL(lin, PAD_TL_MERGED);
+  PAD_TL_NOTE(g, tl_flags | PAD_TL_F_MERGER);
+  PAD_TL(lin, PAD_TL_EXIT);
+#undef PAD_TL_NOTE
 }
 
 // ---------------------------------------------------------------------------
@@ -1440,21 +1512,31 @@ static bool oversubscribed_shape(const pad_decode_dims* d, int num_splits, int n
          d->max_pages < (1 << 23);
 }
 
-static bool latency_bound_shape(const pad_decode_dims* d, int num_cus) {
-  const int max_pages = d->max_pages > 0 ? d->max_pages : 1;
+// Pages of one sequence the plan assumes: the dense table's row width, or
+// for a CSR index (max_pages = entries of `indices`, the whole batch's
+// pages) the mean per sequence, which is exact for equal lengths; ragged
+// CSR batches are re-planned in-kernel from indptr anyway.
+static int plan_pages_per_seq(const pad_decode_dims* d, bool csr) {
+  if (d->max_pages <= 0) return 1;
+  if (!csr || d->batch <= 1) return d->max_pages;
+  return ceil_div(d->max_pages, d->batch);
+}
+
+static bool latency_bound_shape(const pad_decode_dims* d, int num_cus, bool csr) {
+  const int max_pages = plan_pages_per_seq(d, csr);
   const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
   const int64_t blocks_per_seq = ((int64_t)max_pages * d->page_size + kBlockTokens - 1) / kBlockTokens;
   return units * blocks_per_seq <= 16 * (int64_t)num_cus;
 }
 
-static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int engine,
+static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int engine, bool csr,
                      pad_decode_plan_t* p) {
   const int st = validate_dims(d);
   if (st != PAD_OK) return st;
   if (num_splits < 0 || num_splits > PAD_MAX_SPLITS) return PAD_ERR_NUM_SPLITS;
   if (num_cus <= 0) num_cus = 256;
   const int gqa = d->num_q_heads / d->num_kv_heads;
-  const int max_pages = d->max_pages > 0 ? d->max_pages : 1;
+  const int max_pages = plan_pages_per_seq(d, csr);
   const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
 
   // Regimes (fitted to measured split sweeps of C2 batch 1-64, C3 and C4 on
@@ -1465,7 +1547,7 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   // CUs: fewer splits to merge, each streamed by more waves (batch 8: 11.9
   // vs 13.2 us).
   const int64_t blocks_per_seq = ((int64_t)max_pages * d->page_size + kBlockTokens - 1) / kBlockTokens;
-  const bool latency_bound = latency_bound_shape(d, num_cus);
+  const bool latency_bound = latency_bound_shape(d, num_cus, csr);
   int S;
   int pps;
   if (num_splits > 0) {
@@ -1494,6 +1576,13 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     if (s_cap < 1) s_cap = 1;
     if (s_want > s_cap) s_want = s_cap;
     if (s_want > PAD_MAX_SPLITS) s_want = PAD_MAX_SPLITS;
+    if (csr) {
+      // Never more splits (hence scratch) than the dense plan of the same
+      // dims, so pad_decode_workspace_bytes() also sizes a CSR launch.
+      pad_decode_plan_t dense;
+      plan_impl(d, 0, num_cus, engine, false, &dense);
+      if (s_want > dense.num_splits) s_want = dense.num_splits;
+    }
     pps = ceil_div(max_pages, s_want);
     S = ceil_div(max_pages, pps);
   }
@@ -1595,16 +1684,20 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
                        int32_t* counters, int64_t num_counters, const pad_decode_dims* d, float scale,
                        int num_splits, int engine, void* const* events, void* stream) {
   if (engine != 0 && engine != 1) return PAD_ERR_INVALID_SHAPE;
+  // Page ids are bounds-checked against num_pages on the device (an id
+  // outside [0, num_pages) reads page 0), so a launch that reads pages needs
+  // the real cache size.
+  if (d && d->batch > 0 && d->max_pages > 0 && d->num_pages <= 0) return PAD_ERR_INVALID_SHAPE;
   int cus = 0;
   int st = device_cus(&cus);
   if (st != PAD_OK) return st;
+  const bool csr = indptr != nullptr || lpl != nullptr;
   pad_decode_plan_t plan;
-  st = plan_impl(d, num_splits, cus, engine, &plan);
+  st = plan_impl(d, num_splits, cus, engine, csr, &plan);
   if (st != PAD_OK) return st;
   const int gqa = d->num_q_heads / d->num_kv_heads;
   if (engine == 1 && !valu_supported(d->head_dim, gqa)) return PAD_ERR_UNSUPPORTED_GQA;
   if (d->batch == 0) return PAD_OK;
-  const bool csr = indptr != nullptr || lpl != nullptr;
   if (!q || !k || !v || !out) return PAD_ERR_NULL_POINTER;
   if (csr ? (!indptr || !lpl || (!bt && d->max_pages > 0)) : (!bt || !sl)) return PAD_ERR_NULL_POINTER;
   // 16-byte rows: every K/V/q/out row start must be 16-byte aligned.
@@ -1647,7 +1740,7 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.ssl = d->sl_stride;
   a.sob = d->out_stride[0];
   a.soh = d->out_stride[1];
-  a.num_pages = d->num_pages > 0 ? d->num_pages : 1;
+  a.num_pages = d->num_pages;
   a.gqa = gqa;
   a.ps = d->page_size;
   a.pps = plan.pages_per_split;
@@ -1660,7 +1753,7 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   // keeps its meaning (that many page-aligned splits per sequence).
   a.balance = 0;
   if (num_splits == 0 && !plan.single_pass && d->batch <= kPlanMaxBatch && d->max_pages < (1 << 23))
-    a.balance = oversubscribed_shape(d, num_splits, cus, latency_bound_shape(d, cus)) ? 2 : 1;
+    a.balance = oversubscribed_shape(d, num_splits, cus, latency_bound_shape(d, cus, csr)) ? 2 : 1;
   a.min_chunk = ceil_div(kMinBlocks * kBlockTokens, d->page_size);
   a.pair_heads = ((d->head_dim * 2) % 128 != 0 && d->num_kv_heads % 2 == 0 &&
                   ((int64_t)S * d->num_kv_heads * d->batch) % 16 == 0) ? 1 : 0;
@@ -1669,6 +1762,9 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
     if ((1 << sh) == d->page_size) a.ps_shift = sh;
   a.scale_log2 = scale * kLog2e;
   a.nw = plan.waves_per_group;
+#ifdef PAD_TIMELINE
+  a.tl_launch = tl_launches++ % PAD_TL_LAUNCHES;
+#endif
 
   const int nw = plan.waves_per_group;
   const size_t lds = group_lds_bytes(nw, gqa, d->head_dim, engine);
@@ -1698,13 +1794,18 @@ extern "C" {
 
 int pad_decode_plan(const pad_decode_dims* dims, int num_splits, int num_cus, pad_decode_plan_t* plan) {
   if (!plan) return PAD_ERR_NULL_POINTER;
-  return pad::plan_impl(dims, num_splits, num_cus, 0, plan);
+  return pad::plan_impl(dims, num_splits, num_cus, 0, false, plan);
+}
+
+int pad_decode_plan_csr(const pad_decode_dims* dims, int num_splits, int num_cus, pad_decode_plan_t* plan) {
+  if (!plan) return PAD_ERR_NULL_POINTER;
+  return pad::plan_impl(dims, num_splits, num_cus, 0, true, plan);
 }
 
 int pad_decode_workspace_bytes(const pad_decode_dims* dims, int num_splits, int num_cus, size_t* bytes) {
   if (!bytes) return PAD_ERR_NULL_POINTER;
   pad_decode_plan_t p;
-  const int st = pad::plan_impl(dims, num_splits, num_cus, 0, &p);
+  const int st = pad::plan_impl(dims, num_splits, num_cus, 0, false, &p);
   if (st != PAD_OK) return st;
   *bytes = p.workspace_bytes;
   return PAD_OK;
@@ -1713,7 +1814,7 @@ int pad_decode_workspace_bytes(const pad_decode_dims* dims, int num_splits, int 
 int pad_decode_counters_needed(const pad_decode_dims* dims, int num_splits, int num_cus, int64_t* count) {
   if (!count) return PAD_ERR_NULL_POINTER;
   pad_decode_plan_t p;
-  const int st = pad::plan_impl(dims, num_splits, num_cus, 0, &p);
+  const int st = pad::plan_impl(dims, num_splits, num_cus, 0, false, &p);
   if (st != PAD_OK) return st;
   *count = p.counters;
   return PAD_OK;
@@ -1778,5 +1879,24 @@ const char* pad_status_string(int status) {
 }
 
 int pad_decode_abi_version(void) { return PAD_ABI_VERSION; }
+
+#ifdef PAD_TIMELINE
+int pad_timeline_read(void* host, size_t bytes) {
+  if (!host) return PAD_ERR_NULL_POINTER;
+  const size_t n = bytes < sizeof(pad::tl_buf) ? bytes : sizeof(pad::tl_buf);
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(pad::tl_buf), n, 0, hipMemcpyDeviceToHost) == hipSuccess
+             ? PAD_OK
+             : PAD_ERR_DEVICE;
+}
+
+int pad_timeline_reset(void) {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(pad::tl_buf)) != hipSuccess) return PAD_ERR_DEVICE;
+  if (hipMemset(p, 0, sizeof(pad::tl_buf)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+    return PAD_ERR_DEVICE;
+  pad::tl_launches = 0;
+  return PAD_OK;
+}
+#endif
 
 }  // extern "C"

@@ -18,7 +18,9 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include <map>
+#include <mutex>
 #include <utility>
+#include <vector>
 
 #include "pa_decode.h"
 
@@ -38,24 +40,55 @@ int cached_cus(int device) {
 // Per (device, stream) scratch kept across calls: the fp32 partial
 // workspace (no state between launches) and the int32 arrival counters,
 // which start at zero and are left at zero by every launch.  Launches on one
-// stream are ordered, so reusing both on their stream is safe; each grows
-// (a fresh buffer, counters zero-filled, on the same stream) when a call
-// needs more.
+// stream are ordered, so reusing both on their stream is safe.  When a call
+// needs more, a buffer of at least twice the size replaces it (counters
+// zero-filled, on the same stream), and the replaced buffer is kept alive
+// for the rest of the process: a HIP graph captured earlier on this stream
+// holds its raw address and writes partials and counters there on every
+// replay, so returning it to the caching allocator would let those replays
+// corrupt whatever tensor got the memory next.  Growth can therefore never
+// happen during stream capture (the new buffer would also come from the
+// capture's private pool); such a call raises, and one eager call of the
+// largest shape on the capturing stream beforehand sizes the scratch.
 struct StreamScratch {
   torch::Tensor workspace;
   torch::Tensor counters;
+  std::vector<torch::Tensor> retired;  // replaced buffers, still referenced by captured graphs
 };
+
+bool stream_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(stream, &status);
+  TORCH_CHECK(e == hipSuccess, "pa_decode: hipStreamIsCapturing failed: ", hipGetErrorString(e));
+  return status != hipStreamCaptureStatusNone;
+}
 
 StreamScratch& stream_scratch(const torch::Tensor& like, hipStream_t stream, size_t ws_bytes,
                               int64_t num_counters) {
+  static std::mutex mu;
   static std::map<std::pair<int, uintptr_t>, StreamScratch> cache;
+  std::lock_guard<std::mutex> lock(mu);
   StreamScratch& sc = cache[{like.get_device(), reinterpret_cast<uintptr_t>(stream)}];
-  if (!sc.workspace.defined() || static_cast<size_t>(sc.workspace.numel()) < ws_bytes) {
-    const int64_t grown = static_cast<int64_t>(((ws_bytes + (1u << 20) - 1) >> 20) << 20);
+  const bool grow_ws = !sc.workspace.defined() || static_cast<size_t>(sc.workspace.numel()) < ws_bytes;
+  const bool grow_cnt = !sc.counters.defined() || sc.counters.numel() < num_counters;
+  if ((grow_ws || grow_cnt) && stream_capturing(stream)) {
+    TORCH_CHECK(false,
+                "pa_decode: this call needs more split scratch than the capturing stream holds, and scratch "
+                "cannot grow during HIP graph capture (a captured graph keeps the addresses it was captured "
+                "with). Run one eager call with the largest shape on the capture stream before capturing.");
+  }
+  if (grow_ws) {
+    const size_t old = sc.workspace.defined() ? static_cast<size_t>(sc.workspace.numel()) : 0;
+    const size_t want = ws_bytes > 2 * old ? ws_bytes : 2 * old;
+    const int64_t grown = static_cast<int64_t>(((want + (1u << 20) - 1) >> 20) << 20);
+    if (sc.workspace.defined()) sc.retired.push_back(sc.workspace);
     sc.workspace = torch::empty({grown}, like.options().dtype(at::kByte));
   }
-  if (!sc.counters.defined() || sc.counters.numel() < num_counters) {
-    const int64_t grown = ((num_counters + 4095) / 4096) * 4096;
+  if (grow_cnt) {
+    const int64_t old = sc.counters.defined() ? sc.counters.numel() : 0;
+    const int64_t want = num_counters > 2 * old ? num_counters : 2 * old;
+    const int64_t grown = ((want + 4095) / 4096) * 4096;
+    if (sc.counters.defined()) sc.retired.push_back(sc.counters);
     sc.counters = torch::zeros({grown}, like.options().dtype(at::kInt));
   }
   return sc;
@@ -186,7 +219,7 @@ torch::Tensor forward_csr(torch::Tensor q, torch::Tensor k_cache, torch::Tensor 
 
   const int cus = cached_cus(q.get_device());
   pad_decode_plan_t plan;
-  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cus, &plan);
+  int st = pad_decode_plan_csr(&d, static_cast<int>(num_splits), cus, &plan);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
   void* ws_ptr = nullptr;
@@ -220,9 +253,10 @@ torch::Tensor forward_v4(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v
   return forward(q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, 0);
 }
 
-// The plan the launch would use, as a dict (host only).
+// The plan the launch would use, as a dict (host only); with `csr`, the plan
+// of a CSR launch whose `indices` hold max_pages entries.
 py::dict plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-              int64_t page_size, int64_t max_pages, int64_t num_splits, int64_t num_cus) {
+              int64_t page_size, int64_t max_pages, int64_t num_splits, int64_t num_cus, bool csr) {
   pad_decode_dims d;
   std::memset(&d, 0, sizeof(d));
   d.batch = static_cast<int32_t>(batch);
@@ -233,7 +267,8 @@ py::dict plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t 
   d.max_pages = static_cast<int32_t>(max_pages);
   d.q_stride[2] = d.k_stride[3] = d.v_stride[3] = d.out_stride[2] = 1;
   pad_decode_plan_t p;
-  const int st = pad_decode_plan(&d, static_cast<int>(num_splits), static_cast<int>(num_cus), &p);
+  const int st = csr ? pad_decode_plan_csr(&d, static_cast<int>(num_splits), static_cast<int>(num_cus), &p)
+                     : pad_decode_plan(&d, static_cast<int>(num_splits), static_cast<int>(num_cus), &p);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   py::dict r;
   r["num_splits"] = p.num_splits;

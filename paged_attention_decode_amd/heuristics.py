@@ -57,13 +57,23 @@ def group_lds_bytes(nw: int, gqa: int, head_dim: int, engine: int = 0) -> int:
     return nw * (16 * 8 + gqa * (head_dim + 4) * 4 + stage) + q_stage
 
 
+def pages_per_seq(batch: int, max_pages: int, csr: bool) -> int:
+    """Pages of one sequence the plan assumes: the dense row width, or for a CSR index (max_pages = entries of
+    ``indices``) the mean per sequence."""
+    if max_pages <= 0:
+        return 1
+    if not csr or batch <= 1:
+        return max_pages
+    return _cdiv(max_pages, batch)
+
+
 def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int, max_pages: int,
-         num_splits: int = 0, num_cus: int = 256, engine: int = 0) -> Plan:
-    """Same result as ``pad_decode_plan`` for valid arguments."""
+         num_splits: int = 0, num_cus: int = 256, engine: int = 0, csr: bool = False) -> Plan:
+    """Same result as ``pad_decode_plan`` (``pad_decode_plan_csr`` with ``csr``) for valid arguments."""
     if num_cus <= 0:
         num_cus = 256
     gqa = num_q_heads // num_kv_heads
-    mp = max_pages if max_pages > 0 else 1
+    mp = pages_per_seq(batch, max_pages, csr)
     units = max(batch, 1) * num_kv_heads
     blocks_per_seq = _cdiv(mp * page_size, BLOCK_TOKENS)
     latency_bound = units * blocks_per_seq <= 16 * num_cus
@@ -82,6 +92,9 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
             cap = max(cap, min(blocks_per_seq // MIN_BLOCKS_SHORT, 16))
         cap = max(cap, 1)
         want = max(min(want, cap, MAX_SPLITS), 1)
+        if csr:  # never more splits (scratch) than the dense plan of the same dims
+            want = min(want, plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, 0, num_cus,
+                                  engine).num_splits)
         pps = _cdiv(mp, want)
         s = _cdiv(mp, pps)
     nw = _cdiv(pps * page_size, BLOCK_TOKENS)

@@ -158,6 +158,10 @@ def paged_attention_decode_csr(q, k_cache, v_cache, indptr, indices, last_page_l
                              int(engine))
 
 
-def plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits=0, num_cus=0):
-    """Split plan the native launcher would use (host only), as a dict."""
-    return ext().plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits, num_cus)
+def plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits=0, num_cus=0, csr=False):
+    """Split plan the native launcher would use (host only), as a dict.
+
+    With ``csr=True``, the plan of :func:`paged_attention_decode_csr` whose ``indices`` hold ``max_pages``
+    entries (all sequences' pages)."""
+    return ext().plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits, num_cus,
+                      bool(csr))

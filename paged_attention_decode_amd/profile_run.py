@@ -11,17 +11,57 @@ counter should report for a plain stream of known size), then ``--calls``
 decode calls of the named configuration, rotating over enough distinct KV
 caches that the 256 MB Infinity Cache cannot serve repeats ("cold"), or on
 one set of inputs with ``--warm``.  Prints the per-call algorithmic bytes.
+
+``--timeline`` instead runs each configuration of ``--configs`` (e.g.
+``C2:16,C2:32,C3``) through ``libpa_decode_tl.so`` (the decode library with
+per-workgroup phase stamps) in groups of 4 back-to-back cold launches and
+prints the median per-phase budget (timeline.py), one line per
+configuration; ``--json`` also writes the table as JSON.
 """
 
 from __future__ import annotations
 
 import argparse
+import json
 import math
 
 import torch
 
 from . import paged_attention_decode_ex
 from . import workloads as wl
+
+
+def _sets(make, warm: bool):
+    w0 = make(1)
+    n_sets = 1 if warm else max(2, math.ceil(512 * (1 << 20) / (w0.k_cache.numel() * 4)) + 1)
+    return [w0] + [make(1 + i) for i in range(1, n_sets)]
+
+
+def run_timeline(a) -> None:
+    from . import timeline as tl
+
+    rows = {}
+    cols = ("span", "gap", "dispatch", "item", "loop", "loop_tail", "publish", "arrive", "merge", "exit_tail")
+    print("timeline budget, us (medians over %d groups of 4 back-to-back cold launches)" % a.repeats, flush=True)
+    print(f"{'config':8s} {'grid':>6s} {'S':>3s} {'nw':>3s} " + " ".join(f"{c:>9s}" for c in cols), flush=True)
+    for cfg in a.configs.split(","):
+        name, _, b = cfg.partition(":")
+        batch = int(b) if b else None
+        sets = _sets(lambda seed: wl.make(name, batch=batch, seed=seed), a.warm)
+        outs = [torch.empty_like(w.q) for w in sets]
+        recs, groups, plan = tl.record(sets, outs, a.num_splits, a.engine, repeats=a.repeats)
+        med = tl.median_budget(recs)
+        xcc = sorted(set(x for r in recs for x in r["xcc_ids"]))
+        rows[cfg] = {"grid": groups, "num_splits": plan.num_splits, "waves": plan.waves_per_group, **med,
+                     "xcc_ids_seen": xcc}
+        fmt = lambda v: f"{v:9.2f}" if v is not None else f"{'-':>9s}"
+        print(f"{cfg:8s} {groups:6d} {plan.num_splits:3d} {plan.waves_per_group:3d} "
+              + " ".join(fmt(med[c]) for c in cols), flush=True)
+        del sets, outs
+        torch.cuda.empty_cache()
+    if a.json:
+        with open(a.json, "w") as f:
+            json.dump(rows, f, indent=1)
 
 
 def main() -> None:
@@ -34,7 +74,14 @@ def main() -> None:
     p.add_argument("--copy-mb", type=int, default=256)
     p.add_argument("--warm", action="store_true")
     p.add_argument("--shape", default="", help="B/HQ/HKV/D/L[/PS]: uniform lengths instead of --config")
+    p.add_argument("--timeline", action="store_true", help="per-phase budget from libpa_decode_tl.so")
+    p.add_argument("--configs", default="C2:16,C2:32,C2:64,C3,C4", help="--timeline: configurations")
+    p.add_argument("--repeats", type=int, default=8, help="--timeline: groups of 4 launches")
+    p.add_argument("--json", default="", help="--timeline: write the table here")
     a = p.parse_args()
+    if a.timeline:
+        run_timeline(a)
+        return
 
     if a.copy_mb > 0:
         n = a.copy_mb * (1 << 20) // 2
@@ -57,9 +104,8 @@ def main() -> None:
     else:
         def make(seed):
             return wl.make(a.config, batch=a.batch, seed=seed)
-    w0 = make(1)
-    n_sets = 1 if a.warm else max(2, math.ceil(512 * (1 << 20) / (w0.k_cache.numel() * 4)) + 1)
-    sets = [w0] + [make(1 + i) for i in range(1, n_sets)]
+    sets = _sets(make, a.warm)
+    w0, n_sets = sets[0], len(sets)
     torch.cuda.synchronize()
     for i in range(a.calls):
         w = sets[i % n_sets]

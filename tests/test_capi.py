@@ -51,7 +51,7 @@ def test_library_exports_every_declared_symbol():
     lib = _native.capi()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.pad_decode_abi_version() == 2
+    assert lib.pad_decode_abi_version() == 3
 
 
 def test_status_strings():
@@ -100,6 +100,70 @@ def test_plan_matches_python_mirror(batch, hq, hkv, d, ps, max_pages, splits, cu
     assert lib.pad_decode_counters_needed(ctypes.byref(_dims(batch, hq, hkv, d, ps, max_pages)), splits, cus,
                                           ctypes.byref(nc)) == 0
     assert nc.value == m.counters
+
+
+@pytest.mark.parametrize("batch,hq,hkv,d,ps,nnz,splits", [
+    (1, 12, 2, 128, 16, 256, 0),
+    (16, 12, 2, 128, 16, 16 * 256, 0),
+    (64, 12, 2, 128, 16, 64 * 256, 0),
+    (32, 12, 2, 128, 32, 4000, 0),
+    (4, 12, 2, 128, 16, 1000, 0),
+    (3, 8, 1, 64, 8, 10, 0),
+    (5, 12, 2, 128, 16, 300, 3),
+    (256, 64, 8, 128, 16, 256 * 1000, 0),
+    (2, 32, 8, 128, 16, 16384, 0),
+])
+def test_plan_csr_matches_python_mirror(batch, hq, hkv, d, ps, nnz, splits):
+    lib = _native.capi()
+    p = _native.PadPlan()
+    assert lib.pad_decode_plan_csr(ctypes.byref(_dims(batch, hq, hkv, d, ps, nnz)), splits, 256, ctypes.byref(p)) == 0
+    m = heuristics.plan(batch, hq, hkv, d, ps, nnz, splits, 256, csr=True)
+    assert (p.num_splits, p.pages_per_split, p.waves_per_group, bool(p.single_pass), p.workspace_bytes,
+            p.counters) == (m.num_splits, m.pages_per_split, m.waves_per_group, m.single_pass, m.workspace_bytes,
+                            m.counters)
+
+
+def test_plan_csr_uses_pages_per_sequence():
+    # 16 sequences of 256 pages as a CSR index of 4096 entries plan like the
+    # dense table of 256 columns (the whole index is not one sequence).
+    dense = heuristics.plan(16, 12, 2, 128, 16, 256)
+    csr = heuristics.plan(16, 12, 2, 128, 16, 16 * 256, csr=True)
+    assert (csr.num_splits, csr.pages_per_split, csr.waves_per_group) == (
+        dense.num_splits, dense.pages_per_split, dense.waves_per_group)
+    # Small batches plan like their dense twins too (latency-bound shapes:
+    # short splits, up to 8 waves).
+    for batch, width in ((2, 64), (4, 256), (1, 100)):
+        d2 = heuristics.plan(batch, 12, 2, 128, 16, width)
+        c2 = heuristics.plan(batch, 12, 2, 128, 16, batch * width, csr=True)
+        assert (c2.num_splits, c2.pages_per_split, c2.waves_per_group) == (
+            d2.num_splits, d2.pages_per_split, d2.waves_per_group), (batch, width)
+    assert heuristics.plan(4, 12, 2, 128, 16, 4 * 256, csr=True).waves_per_group == 8
+
+
+def test_plan_csr_scratch_never_exceeds_dense():
+    # pad_decode_workspace_bytes() / pad_decode_counters_needed() on the
+    # dense reading of the dims must size every CSR launch.
+    for batch in (1, 2, 3, 4, 8, 16, 33, 64, 128, 256, 300):
+        for hkv in (1, 2, 8):
+            for nnz in (1, 7, 64, 256, 1000, 4096, 20000, 200000):
+                for ps in (1, 16, 32):
+                    for splits in (0, 4):
+                        c = heuristics.plan(batch, 8 * hkv, hkv, 128, ps, nnz, splits, 256, csr=True)
+                        dn = heuristics.plan(batch, 8 * hkv, hkv, 128, ps, nnz, splits, 256)
+                        assert c.workspace_bytes <= dn.workspace_bytes and c.counters <= dn.counters, (
+                            batch, hkv, nnz, ps, splits)
+
+
+def test_launch_rejects_zero_num_pages_on_the_host():
+    # num_pages bounds the page ids on the device; 0 would silently read
+    # page 0 for every page, so the launch refuses it before any device call.
+    lib = _native.capi()
+    dm = _dims(batch=2, max_pages=4, num_pages=0)
+    fake = ctypes.c_void_p(256)
+    assert lib.pad_decode_launch(fake, fake, fake, fake, fake, fake, None, 0, None, 0, ctypes.byref(dm), 0.1, 1,
+                                 None) == 2
+    assert lib.pad_decode_launch_csr(fake, fake, fake, fake, fake, fake, fake, None, 0, None, 0, ctypes.byref(dm),
+                                     0.1, 1, 0, None) == 2
 
 
 @pytest.mark.parametrize("d", [32, 64, 96, 128, 256])

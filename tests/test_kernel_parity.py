@@ -391,6 +391,53 @@ def test_graph_capture_replays(case):
                                                    torch.tensor(lens, dtype=torch.int32)))
 
 
+def test_graph_replay_survives_scratch_growth_and_capture_refuses_growth():
+    # A graph captured with the stream's small scratch keeps that address.
+    # A later, larger eager call on the same stream grows the scratch; the
+    # replaced buffer must stay alive (not go back to the caching allocator),
+    # so replays still write their partials and counters somewhere private.
+    # Growing during capture itself is refused with a clear error.
+    import paged_attention_decode_amd as pad
+
+    def case(lens, seed):
+        bt, n = shuffled_table(lens, 16, spare_pages=1, extra_cols=0, seed=seed)
+        k, v = make_cache(n, 16, 2, 128, seed=seed)
+        q = torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(seed))
+        sl = torch.tensor(lens, dtype=torch.int32)
+        return [q.half().cuda(), k.half().cuda(), v.half().cuda(), bt.cuda(), sl.cuda()], (q, k, v, bt, sl)
+
+    small, small_cpu = case([700, 1500], 301)
+    big, big_cpu = case([4096] * 48, 302)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        pad.paged_attention_decode(*small)  # sizes this stream's scratch for the small shape only
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out_static = pad.paged_attention_decode(*small)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        big_out = pad.paged_attention_decode(*big)  # grows the scratch of stream s
+        # Allocations that could reuse the replaced scratch, written with a pattern.
+        fillers = [torch.full((1 << 18,), 7.0, device="cuda") for _ in range(16)]
+    torch.cuda.synchronize()
+    expected_small = decode_fp16_protocol(*small_cpu)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_parity(out_static, expected_small)
+        assert all(bool((f == 7.0).all()) for f in fillers), "a replay wrote into memory it no longer owns"
+    assert_parity(big_out, decode_fp16_protocol(*big_cpu))
+    # Capturing a call whose scratch would have to grow raises.
+    fresh = torch.cuda.Stream()
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="graph capture"):
+        with torch.cuda.graph(g2, stream=fresh):
+            pad.paged_attention_decode(*small)
+    torch.cuda.synchronize()
+
+
 def test_mixed_call_shapes_share_scratch():
     # Calls of different shapes reuse the binding's per-stream scratch: a call
     # with few long sequences (many partials) followed by calls with many
