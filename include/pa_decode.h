@@ -78,8 +78,15 @@ typedef enum pad_status {
   PAD_ERR_WORKSPACE = 7,         /* workspace or counters NULL / too small */
   PAD_ERR_NUM_SPLITS = 8,        /* num_splits < 0 or > PAD_MAX_SPLITS     */
   PAD_ERR_LAUNCH = 9,            /* the HIP runtime rejected a launch      */
-  PAD_ERR_DEVICE = 10            /* no usable device / device query failed */
+  PAD_ERR_DEVICE = 10,           /* no usable device / device query failed */
+  PAD_ERR_SCRATCH_LIMIT = 11     /* pad_decode_launch_noalloc: the call needs
+                                    more than its static scratch holds      */
 } pad_status;
+
+/* Static scratch of pad_decode_launch_noalloc(), per device: fp32 partials
+ * and int32 arrival counters.  48 MiB in all, held until the process ends. */
+#define PAD_NOALLOC_WORKSPACE_BYTES ((size_t)48 * 1024 * 1024 - (size_t)256 * 1024)
+#define PAD_NOALLOC_COUNTERS 65536
 
 /* Shapes and element strides of one call (a plain tensor descriptor). */
 typedef struct pad_decode_dims {
@@ -161,6 +168,27 @@ int pad_decode_workspace_bytes(const pad_decode_dims* dims, int num_splits,
  * needed no arrival counting. */
 int pad_decode_counters_needed(const pad_decode_dims* dims, int num_splits,
                                int num_cus, int64_t* count);
+
+/* pad_decode_launch() without workspace or counters arguments: it allocates
+ * nothing (no hipMalloc/hipFree, no allocating library call), for callers
+ * that cannot allocate - code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.  No counterpart in the reference (its
+ * launcher allocated the partials on every call,
+ * cuda/kernel_v4_split_k.cu:228-232).  The split scratch is a static device
+ * array of the library, one per GPU, of PAD_NOALLOC_WORKSPACE_BYTES bytes of
+ * partials and PAD_NOALLOC_COUNTERS counters; a call whose plan
+ * (pad_decode_workspace_bytes() / pad_decode_counters_needed()) needs more
+ * returns PAD_ERR_SCRATCH_LIMIT without launching.  The first call on a
+ * device looks up its copy's address and queues a small kernel that zeroes
+ * the counters on `stream`.  Every call on one GPU shares that GPU's array:
+ * calls that may overlap on one GPU (different streams, or graphs replayed
+ * concurrently) race and must be serialised by the caller.  Same kernels,
+ * plan and results as pad_decode_launch(). */
+int pad_decode_launch_noalloc(const void* q, const void* k_cache,
+                              const void* v_cache, const int32_t* block_table,
+                              const int32_t* seq_lens, void* out,
+                              const pad_decode_dims* dims, float scale,
+                              int num_splits, void* stream);
 
 /* Zero `num_counters` counters (asynchronously, on `stream`); needed once
  * per counter buffer. */

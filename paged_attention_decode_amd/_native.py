@@ -113,6 +113,8 @@ SIGNATURES = {
          ctypes.c_float, ctypes.c_int, ctypes.c_int, _VP],
         ctypes.c_int,
     ),
+    "pad_decode_launch_noalloc": (
+        [_VP, _VP, _VP, _VP, _VP, _VP, ctypes.POINTER(PadDims), ctypes.c_float, ctypes.c_int, _VP], ctypes.c_int),
     "pad_device_num_cus": ([ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "pad_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "pad_decode_abi_version": ([], ctypes.c_int),

@@ -47,6 +47,8 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "pa_decode.h"
 #include "pa_decode_timeline.h"  // slot constants; its functions exist only with -DPAD_TIMELINE
 
@@ -1788,6 +1790,71 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   return PAD_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free launches (pad_decode_launch_noalloc): the split scratch is
+// a file-scope device array instead of caller memory.  Layout: the int32
+// arrival counters first (PAD_NOALLOC_COUNTERS of them), then the partials
+// workspace (PAD_NOALLOC_WORKSPACE_BYTES).  Every GPU the library runs on
+// holds its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in, not device memory: the per-device address comes from
+// hipGetSymbolAddress once per device and only that address is used.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoallocCounterBytes = (size_t)PAD_NOALLOC_COUNTERS * sizeof(int32_t);
+static __device__ __align__(256) unsigned char scratch[kNoallocCounterBytes + PAD_NOALLOC_WORKSPACE_BYTES];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Zeroes n int32 values with vector stores (used for the counters once per
+// device; a kernel rather than hipMemsetAsync so that a call made under
+// stream capture records a kernel node).
+__global__ void pad_zero_i32_kernel(int32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+// The current device's scratch address; the first call on a device looks it
+// up (with that device current) and queues a clear of its counters on
+// `stream`, ahead of the caller's launch.  The array is zero when the code
+// object loads, and every launch leaves the counters zero again, so the
+// clear only makes that state explicit.
+static int noalloc_scratch(hipStream_t stream, unsigned char** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return PAD_ERR_DEVICE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return PAD_ERR_DEVICE;
+    hipLaunchKernelGGL(pad_zero_i32_kernel, dim3(64), dim3(256), 0, stream, static_cast<int32_t*>(ptr),
+                       (int64_t)PAD_NOALLOC_COUNTERS);
+    if (hipGetLastError() != hipSuccess) return PAD_ERR_LAUNCH;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = static_cast<unsigned char*>(g_scratch_ptr[dev]);
+  return PAD_OK;
+}
+
+static int launch_noalloc(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
+                          void* out, const pad_decode_dims* d, float scale, int num_splits, void* stream) {
+  if (d && d->batch > 0 && d->max_pages > 0 && d->num_pages <= 0) return PAD_ERR_INVALID_SHAPE;
+  int cus = 0;
+  int st = device_cus(&cus);
+  if (st != PAD_OK) return st;
+  pad_decode_plan_t plan;
+  st = plan_impl(d, num_splits, cus, 0, false, &plan);
+  if (st != PAD_OK) return st;
+  if (plan.workspace_bytes > PAD_NOALLOC_WORKSPACE_BYTES || plan.counters > PAD_NOALLOC_COUNTERS)
+    return PAD_ERR_SCRATCH_LIMIT;
+  unsigned char* base = nullptr;
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  st = noalloc_scratch(hs, &base);
+  if (st != PAD_OK) return st;
+  return launch_impl(q, k, v, bt, sl, nullptr, nullptr, out, base + kNoallocCounterBytes,
+                     PAD_NOALLOC_WORKSPACE_BYTES, reinterpret_cast<int32_t*>(base), PAD_NOALLOC_COUNTERS, d, scale,
+                     num_splits, 0, nullptr, stream);
+}
+
 }  // namespace pad
 
 extern "C" {
@@ -1845,6 +1912,12 @@ int pad_decode_launch_ex(const void* q, const void* k_cache, const void* v_cache
                           workspace_bytes, counters, num_counters, dims, scale, num_splits, engine, events, stream);
 }
 
+int pad_decode_launch_noalloc(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                              const int32_t* seq_lens, void* out, const pad_decode_dims* dims, float scale,
+                              int num_splits, void* stream) {
+  return pad::launch_noalloc(q, k_cache, v_cache, block_table, seq_lens, out, dims, scale, num_splits, stream);
+}
+
 int pad_decode_counters_init(int32_t* counters, int64_t num_counters, void* stream) {
   if (!counters) return PAD_ERR_NULL_POINTER;
   if (num_counters <= 0) return PAD_OK;
@@ -1874,6 +1947,9 @@ const char* pad_status_string(int status) {
     case PAD_ERR_NUM_SPLITS: return "num_splits must be in [0, 1024]";
     case PAD_ERR_LAUNCH: return "kernel launch failed";
     case PAD_ERR_DEVICE: return "no usable HIP device";
+    case PAD_ERR_SCRATCH_LIMIT:
+      return "the call needs more split scratch than pad_decode_launch_noalloc's static buffer holds "
+             "(PAD_NOALLOC_WORKSPACE_BYTES of partials, PAD_NOALLOC_COUNTERS counters); use pad_decode_launch";
     default: return "unknown status";
   }
 }

@@ -57,7 +57,7 @@ def test_library_exports_every_declared_symbol():
 def test_status_strings():
     lib = _native.capi()
     assert lib.pad_status_string(0) == b"ok"
-    for code in range(1, 11):
+    for code in range(1, 12):
         assert lib.pad_status_string(code) not in (b"ok", b"unknown status")
     assert lib.pad_status_string(999) == b"unknown status"
 
