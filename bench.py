@@ -13,18 +13,32 @@ What one run measures (one GPU; ``--gpus`` above 1 exits with a message):
   so the number is an HBM figure ("cold"), not a cache figure.
 * ``roofline``: the decode kernel (one launch per call: split-K phase 1
   with the log-sum-exp merge fused in) - algorithmic bytes per call divided
-  by its mean launch duration, timed with HIP events on the launch stream
-  around the K back-to-back calls of the timed region; peak 8000 GB/s.
-  ``traffic`` comes from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-  committed in profiles/traffic.json when present.
-* ``us_per_call``: the reference's latency method (bench/bench_decode.py:
-  86-112 of the reference): each call bracketed by events and followed by a
-  sync, best of 30 after 10 warm-up calls, median of 15 trials, warm inputs,
-  for every batch of the C2 sweep; plus cold GB/s per batch.
+  by the time per call, timed with HIP events on the launch stream around
+  the K back-to-back calls of the timed region (``us_per_call``: it includes
+  the gap between consecutive kernels, so it is at least the kernel
+  duration); peak 8000 GB/s.  ``traffic`` (HBM bytes per call) is not
+  measured in this run: it is the rocprofv3 FETCH_SIZE / WRITE_SIZE figure
+  committed in profiles/traffic.json (``traffic_source`` names the file and
+  the commit that last changed it); ``fetch_gbs`` = traffic / us_per_call,
+  north_star's "FETCH_SIZE / kernel time" with the same conservative time.
+  ``kernel_trace_us`` is the mean kernel duration rocprofv3 measured for
+  the same configuration (profiles/pad_phase1_kernel_configs_kernel_trace.txt).
+* ``c2_sweep``: for every batch of C2, the reference's latency method
+  (bench/bench_decode.py:86-112 of the reference: each call bracketed by
+  events and followed by a sync, best of 30 after 10 warm-up calls, median
+  of 15 trials, warm inputs) and the cold steady-state throughput of
+  ``--sweep-calls`` back-to-back calls (rotated KV caches), independent of
+  ``--steps`` so that the first call's host-side latency is spread over
+  enough calls.
 * ``cpu_baseline``: the fp32 CPU oracle (oracle/reference.py, a restatement
   of the reference's src/reference.py) timed on the host cores on the same
   headline inputs for a bounded sample (about --cpu-seconds of work), in the
-  same GB/s unit.
+  same GB/s unit.  It uses every core of the process's CPU affinity up to
+  --cpu-threads (16: the share of a GPU box's cores that one GPU gets);
+  ``host`` records os.cpu_count(), the affinity size and the threads used.
+* ``gpu``: device metadata (torch device properties, and amd-smi's static
+  and metric readings when the tool answers), as the reference's bench
+  records nvidia-smi's (bench/measure_peak_bw.py:27-42).
 * ``roofline.measured_ceiling_gbs``: what a read-only kernel with the
   decode's own access pattern (K and V tiles of the same pages, no
   arithmetic; libpa_probe.so via roofline.ceilings) reaches on the same
@@ -41,6 +55,7 @@ import json
 import math
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -68,7 +83,10 @@ def _parse():
     p.add_argument("--no-ceiling", action="store_true", help="skip the measured read ceiling")
     p.add_argument("--no-ragged", action="store_true", help="skip the C3 ragged line")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--cpu-threads", type=int, default=16,
+                   help="most CPU threads for the baseline (a GPU box grants one GPU 16 cores)")
     p.add_argument("--trials", type=int, default=15)
+    p.add_argument("--sweep-calls", type=int, default=200, help="cold back-to-back calls per C2 sweep batch")
     return p.parse_args()
 
 
@@ -121,24 +139,113 @@ def _latency_reference_method(pad, w, engine, splits, trials):
     return statistics.median([once() for _ in range(trials)]) * 1e3  # µs
 
 
-def _traffic(workload_name):
-    path = os.path.join(REPO, "profiles", "traffic.json")
-    if not os.path.exists(path):
+def _git_last_commit(relpath):
+    try:
+        out = subprocess.run(["git", "-C", REPO, "log", "-1", "--format=%h %cs", "--", relpath],
+                             capture_output=True, text=True, timeout=10)
+        return out.stdout.strip() or None
+    except (OSError, subprocess.SubprocessError):
         return None
+
+
+def _traffic(workload_name):
+    """(bytes per call, provenance) from the committed rocprofv3 traffic summary, or (None, None)."""
+    rel = os.path.join("profiles", "traffic.json")
+    path = os.path.join(REPO, rel)
+    if not os.path.exists(path):
+        return None, None
     try:
         data = json.load(open(path))
         rec = data.get(workload_name)
-        return None if rec is None else int(rec["bytes_per_call"])
+        if rec is None:
+            return None, None
+        # The summary records the commit it was measured at; the GPU box has no .git to ask.
+        commit = rec.get("commit") or _git_last_commit(rel)
+        src = f"{rel} ({rec.get('source', 'rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE')}"
+        src += f"; fetch x{rec.get('fetch_scale')}, write x{rec.get('write_scale')}"
+        src += f"; commit {commit})" if commit else ")"
+        return int(rec["bytes_per_call"]), src
     except (ValueError, KeyError, TypeError):
+        return None, None
+
+
+def _kernel_trace_us(workload_name):
+    """Mean kernel duration rocprofv3 recorded for this configuration in the committed kernel-trace summary."""
+    path = os.path.join(REPO, "profiles", "pad_phase1_kernel_configs_kernel_trace.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.split()
+        if len(f) > 3 and f[0] == workload_name:
+            try:
+                return float(f[2])
+            except ValueError:
+                return None
+    return None
+
+
+def _run_json(cmd, timeout=30):
+    try:
+        out = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+        if out.returncode != 0:
+            return None
+        return json.loads(out.stdout)
+    except (OSError, subprocess.SubprocessError, ValueError):
         return None
 
 
-def _cpu_baseline(w, seconds, gpu_out):
+def _gpu_metadata():
+    """Device properties plus amd-smi's static / metric readings (each omitted if the tool does not answer)."""
+    import torch
+
+    props = torch.cuda.get_device_properties(0)
+    meta = {
+        "name": props.name,
+        "arch": getattr(props, "gcnArchName", None),
+        "compute_units": props.multi_processor_count,
+        "total_memory_gib": round(props.total_memory / 2**30, 1),
+        "torch": torch.__version__,
+        "hip_runtime": getattr(torch.version, "hip", None),
+    }
+    def pick(d, *path):
+        for k in path:
+            if not isinstance(d, dict) or k not in d:
+                return None
+            d = d[k]
+        return d
+
+    static = _run_json(["amd-smi", "static", "--gpu", "0", "--json"])
+    if static is not None:
+        g = (static.get("gpu_data") or [{}])[0] if isinstance(static, dict) else {}
+        meta["amd_smi"] = {
+            "market_name": pick(g, "asic", "market_name"),
+            "device_id": pick(g, "asic", "device_id"),
+            "target": pick(g, "asic", "target_graphics_version"),
+            "num_compute_units": pick(g, "asic", "num_compute_units"),
+            "ifwi": pick(g, "ifwi", "version"),
+            "driver": pick(g, "driver", "name"),
+            "vram": {k: pick(g, "vram", k) for k in ("type", "vendor", "size", "max_bandwidth")},
+        }
+    metric = _run_json(["amd-smi", "metric", "--gpu", "0", "--json"])
+    if metric is not None:
+        g = (metric.get("gpu_data") or [{}])[0] if isinstance(metric, dict) else {}
+        meta.setdefault("amd_smi", {})["after_run"] = {
+            "socket_power": pick(g, "power", "socket_power"),
+            "gfx_clk": pick(g, "clock", "gfx_0", "clk"),
+            "gfx_max_clk": pick(g, "clock", "gfx_0", "max_clk"),
+            "mem_clk": pick(g, "clock", "mem_0", "clk"),
+            "hotspot_temp": pick(g, "temperature", "hotspot"),
+            "mem_temp": pick(g, "temperature", "mem"),
+        }
+    return meta
+
+
+def _cpu_baseline(w, seconds, gpu_out, max_threads):
     import torch
 
     from oracle.reference import paged_attention_decode_reference
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = max(1, min(len(os.sched_getaffinity(0)), max_threads))
     torch.set_num_threads(cores)
     q = w.q.float().cpu()
     k = w.k_cache.float().cpu()
@@ -189,7 +296,7 @@ def main():
     sec = _throughput(pad, sets, engine, splits, args.steps, args.warmup)
     wall = time.perf_counter() - t0
     value = nbytes / sec / 1e9
-    traffic = _traffic(probe.name)
+    traffic, traffic_src = _traffic(probe.name)
 
     result = {
         "metric": METRIC,
@@ -202,7 +309,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16 (fp32 accumulate)",
+        "dtype": "fp16 q/K/V and output, fp32 accumulation; P rounded to fp16 for the PV MFMA",
         "data": "synthetic (seeded N(0,1) fp16, shuffled block tables)",
         "config": {
             "workload": f"C2: batch {args.batch}, seq_len 4096, GQA 12/2, head_dim 128, page 16; "
@@ -228,7 +335,10 @@ def main():
             "unit": "GB/s",
             "frac": round(value / PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel_us": round(sec * 1e6, 3),
+            "traffic_source": traffic_src,
+            "fetch_gbs": round(traffic / sec / 1e9, 1) if traffic else None,
+            "us_per_call": round(sec * 1e6, 3),
+            "kernel_trace_us": _kernel_trace_us(probe.name),
             "timed_region_wall_s": round(wall, 4),
         },
     }
@@ -245,8 +355,8 @@ def main():
     if not args.no_ragged:
         first = wl.make("C3", seed=1000)
         rs = [first] + [wl.make("C3", seed=1000 + i) for i in range(1, _rotation(first.k_cache.numel() * 4))]
-        calls = max(20, args.steps // 2)
-        dense = _throughput(pad, rs, engine, splits, calls, 10)
+        calls = args.sweep_calls
+        dense = _throughput(pad, rs, engine, splits, calls, 20)
         csr_args = [pad.paged_kv_indices(w.block_table, w.seq_lens, w.k_cache.shape[1]) for w in rs]
         for i in range(10):
             j = i % len(rs)
@@ -278,7 +388,7 @@ def main():
             w = wl.make("C2", batch=b, seed=2000 + b)
             lat = _latency_reference_method(pad, w, engine, splits, args.trials)
             rs = [w] + _make_sets(wl.make, _rotation(w.k_cache.numel() * 4) - 1, name="C2", batch=b)
-            cold = _throughput(pad, rs, engine, splits, max(20, args.steps // 2), 5)
+            cold = _throughput(pad, rs, engine, splits, args.sweep_calls, 20)
             nb = wl.bytes_of(w)
             sweep[str(b)] = {
                 "us_per_call_warm": round(lat, 2),
@@ -292,7 +402,7 @@ def main():
     if not args.no_cpu:
         gpu_out = _call(pad, probe, engine, splits)
         torch.cuda.synchronize()
-        med, n, threads, err = _cpu_baseline(probe, args.cpu_seconds, gpu_out)
+        med, n, threads, err = _cpu_baseline(probe, args.cpu_seconds, gpu_out, args.cpu_threads)
         result["cpu_baseline"] = {
             "value": round(nbytes / med / 1e9, 3),
             "unit": "GB/s",
@@ -303,6 +413,13 @@ def main():
             "ms_per_call": round(med * 1e3, 2),
             "gpu_vs_cpu_max_abs_err": err,
         }
+    result["host"] = {
+        "os_cpu_count": os.cpu_count(),
+        "affinity_cores": len(os.sched_getaffinity(0)),
+        "cpu_baseline_threads": result.get("cpu_baseline", {}).get("cores"),
+        "why_capped": f"a GPU box grants one GPU {args.cpu_threads} cores (OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS')})",
+    }
+    result["gpu"] = _gpu_metadata()
     print(json.dumps(result), flush=True)
 
 

@@ -25,7 +25,8 @@ def _decode(w, num_splits=None):
     return pad.paged_attention_decode(*w.args(), num_splits=num_splits)
 
 
-@pytest.mark.parametrize("name,batch", [("C1", None), ("C2", 1), ("C2", 16), ("C2", 64), ("C3", None)])
+@pytest.mark.parametrize("name,batch", [("C1", None), ("C2", 1), ("C2", 2), ("C2", 4), ("C2", 8), ("C2", 16),
+                                        ("C2", 32), ("C2", 64), ("C3", None)])
 def test_config_against_oracle(name, batch):
     from paged_attention_decode_amd import workloads as wl
 

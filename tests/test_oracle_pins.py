@@ -203,3 +203,29 @@ def test_brute_f64_vs_sdpa_f64(seed):
     want = sdpa_check(q.double(), k.double(), v.double(), bt, sl)
     got = decode_f64(q.numpy(), k.numpy(), v.numpy(), bt.numpy(), sl.numpy())
     np.testing.assert_allclose(got, want.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_row_subset_oracle_matches_full_oracle():
+    # decode_rows_fp16_protocol (the C5 subset oracle) relabels the selected
+    # rows' pages onto a compact cache.  It must give exactly the rows of the
+    # full oracle, here with two sequences sharing physical pages, unused
+    # columns pointing at other pages, an empty row, a partial last page and
+    # rows asked for out of order.
+    from oracle.reference import decode_fp16_protocol, decode_rows_fp16_protocol
+
+    lens = [37, 0, 64, 5, 50, 17]
+    ps, hkv, group, d = 16, 2, 3, 32
+    bt, num_pages = shuffled_table(lens, ps, spare_pages=3, extra_cols=2, seed=31)
+    bt[4, :2] = bt[0, :2]  # sequences 0 and 4 share their first two pages
+    k, v = make_cache(num_pages, ps, hkv, d, seed=31)
+    q = torch.randn(len(lens), hkv * group, d, generator=torch.Generator().manual_seed(32))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    full = decode_fp16_protocol(q, k, v, bt, sl)
+    for rows in ([4, 0], [1], [5, 2, 3], [0, 1, 2, 3, 4, 5], [3, 3]):
+        sub = decode_rows_fp16_protocol(q, k, v, bt, sl, rows)
+        assert sub.shape == (len(rows), hkv * group, d)
+        assert torch.equal(sub, full[rows]), rows
+    # A planted mistake (the relabelled table shifted by one page) is caught.
+    bt_bad = bt.clone()
+    bt_bad[0, 0] = bt[0, 1]
+    assert not torch.allclose(decode_rows_fp16_protocol(q, k, v, bt_bad, sl, [0]), full[[0]], atol=1e-3)
