@@ -95,7 +95,7 @@ constexpr int kMinBlocksShort = 4;
 // Units with more splits than this merge in two levels (groups of 16).
 constexpr int kTwoLevelSplits = 48;
 // LDS of one workgroup (wave merge + MFMA staging) is capped so that the
-// widest rows (head_dim 256, 16-row groups) still get 5 waves in a
+// widest rows (head_dim 256, 16-row groups) still get 4 waves in a
 // workgroup that fits a CU's 160 KB: one 2-wave workgroup per split left
 // those shapes latency-bound (16/1 d256 batch 8 x 8192: 35.2 against
 // 24.7 us).
@@ -1172,11 +1172,18 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int
 }
 
 // Minimum waves per SIMD each phase-1 instantiation is compiled for (it
-// caps the registers per lane at 512 / waves).  The split heuristic sizes the
-// grid to one round of resident waves using the same numbers.
-constexpr int phase1_waves_per_simd(int d, int engine) {
-  return engine == 0 ? (d <= 128 ? 3 : 1) : 1;
+// caps the registers per lane at 512 / waves).  The generic page-size mode
+// of head_dim 128 gets 2 (256 registers): its six prefetched page ids did
+// not fit 168 registers without one VGPR spilled to scratch.
+constexpr int phase1_waves_per_simd(int d, int engine, int mode) {
+  return engine == 0 ? (d <= 128 ? (d == 128 && mode == 0 ? 2 : 3) : 1) : 1;
 }
+
+// Most waves in one workgroup.  head_dim 256 takes at most 4, so that each
+// SIMD runs one wave of the workgroup and that wave has the whole register
+// file (256 VGPRs plus AGPRs for spills): with 5 or more waves two share a
+// SIMD's 256 VGPRs, and the loop spilled 7-10 VGPRs to scratch memory.
+constexpr int max_group_waves(int d) { return d >= 256 ? 4 : kMaxWaves; }
 
 // The (split, kv head, sequence) of this workgroup.  Normally the grid
 // coordinates.  With pair_heads (head_dim rows that are not a multiple of
@@ -1204,7 +1211,8 @@ __device__ __forceinline__ void grid_pos(const Phase1Args& a, int& s, int& h, in
 
 // Phase 1: one workgroup per (split, kv head, sequence).
 template <int D, int MODE, int ENGINE, int GQA_T>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE))))
+__global__ __launch_bounds__(max_group_waves(D) * 64)
+    __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE, MODE))))
 void pad_phase1_kernel(const Phase1Args a) {
 #ifdef PAD_TIMELINE
   const unsigned long long tl_entry = __builtin_amdgcn_s_memrealtime();
@@ -1459,7 +1467,7 @@ static size_t group_lds_bytes(int nw, int gqa, int d, int engine) {
 static int lds_wave_cap(int gqa, int d, int engine) {
   const size_t per_wave = group_lds_bytes(1, gqa, d, engine) - group_lds_bytes(0, gqa, d, engine);
   int cap = (int)((kLdsBudget - group_lds_bytes(0, gqa, d, engine)) / per_wave);
-  if (cap > kMaxWaves) cap = kMaxWaves;
+  if (cap > max_group_waves(d)) cap = max_group_waves(d);
   if (cap < 1) cap = 1;
   return cap;
 }

@@ -102,7 +102,8 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     nw = min(nw, MAX_WAVES if latency_bound or narrow_rows else MAX_WAVES // 2)
     fixed = group_lds_bytes(0, gqa, head_dim, engine)
     per_wave = group_lds_bytes(1, gqa, head_dim, engine) - fixed
-    cap_w = max(min((LDS_BUDGET - fixed) // per_wave, MAX_WAVES), 1)
+    # head_dim 256: at most 4 waves, one per SIMD, so a wave has the whole register file
+    cap_w = max(min((LDS_BUDGET - fixed) // per_wave, 4 if head_dim >= 256 else MAX_WAVES), 1)
     nw = max(min(nw, cap_w), 1)
     single = s == 1
     ws = 0 if single else workspace_bytes(batch, num_kv_heads, gqa, head_dim, s)
