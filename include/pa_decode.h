@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PAD_ABI_VERSION 3
+#define PAD_ABI_VERSION 4
 
 /* Largest supported GQA group (query heads per KV head); the reference's
  * bound is the same (cuda/kernel_v4_split_k.cu:44). */
@@ -241,6 +241,58 @@ int pad_decode_launch_csr(const void* q, const void* k_cache,
                           int32_t* counters, int64_t num_counters,
                           const pad_decode_dims* dims, float scale,
                           int num_splits, int engine, void* stream);
+
+/* Plan once, run many: the split between FlashInfer's
+ * BatchDecodeWithPagedKVCacheWrapper.plan() and .run() that the reference's
+ * adapter calls (src/flashinfer_adapter.py:100-112) and its benchmark
+ * amortises over many runs (bench/bench_flashinfer.py:131-151).
+ *
+ * pad_decode_plan_worklist() (dense table) / pad_decode_plan_worklist_csr()
+ * (CSR index) queue one small kernel on `stream` that writes the work list
+ * of a decode with these dims, indices and num_splits into `worklist`
+ * (device memory of pad_decode_worklist_bytes() bytes; pass csr = 1 for a
+ * CSR plan): for every workgroup of the decode grid, the page range and
+ * unit it processes and the page ids its waves read first - what the decode
+ * kernel otherwise works out from the sequence lengths at the start of
+ * every launch.  pad_decode_launch_worklist() / _csr() then run the decode
+ * (MFMA engine) from the list, once per layer of a decode step.  The
+ * results are the same as pad_decode_launch() / pad_decode_launch_csr()
+ * with the same arguments.
+ *
+ * The list encodes the sequence lengths and page ids it was planned from:
+ * plan again after they change (in a decoding loop, once per step, before
+ * the step's first layer).  A list planned for other dims or num_splits is
+ * detected (a key in its header) and ignored: the launch then plans in the
+ * kernel as pad_decode_launch() does.  No counterparts in the reference. */
+int pad_decode_worklist_bytes(const pad_decode_dims* dims, int num_splits,
+                              int num_cus, int csr, size_t* bytes);
+int pad_decode_plan_worklist(const int32_t* block_table,
+                             const int32_t* seq_lens,
+                             const pad_decode_dims* dims, int num_splits,
+                             void* worklist, size_t worklist_bytes,
+                             void* stream);
+int pad_decode_plan_worklist_csr(const int32_t* indices, const int32_t* indptr,
+                                 const int32_t* last_page_len,
+                                 const pad_decode_dims* dims, int num_splits,
+                                 void* worklist, size_t worklist_bytes,
+                                 void* stream);
+int pad_decode_launch_worklist(const void* q, const void* k_cache,
+                               const void* v_cache, const int32_t* block_table,
+                               const int32_t* seq_lens, void* out,
+                               void* workspace, size_t workspace_bytes,
+                               int32_t* counters, int64_t num_counters,
+                               const pad_decode_dims* dims, float scale,
+                               int num_splits, const void* worklist,
+                               size_t worklist_bytes, void* stream);
+int pad_decode_launch_worklist_csr(const void* q, const void* k_cache,
+                                   const void* v_cache, const int32_t* indices,
+                                   const int32_t* indptr,
+                                   const int32_t* last_page_len, void* out,
+                                   void* workspace, size_t workspace_bytes,
+                                   int32_t* counters, int64_t num_counters,
+                                   const pad_decode_dims* dims, float scale,
+                                   int num_splits, const void* worklist,
+                                   size_t worklist_bytes, void* stream);
 
 /* Compute units of the current device (cached per device). */
 int pad_device_num_cus(int* num_cus);

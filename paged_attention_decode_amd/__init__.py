@@ -6,6 +6,7 @@ hand-written gfx950 HIP kernels through the C ABI in include/pa_decode.h.
 """
 
 from .ops import (  # noqa: F401
+    BatchDecodeWrapper,
     ENGINE_MFMA,
     ENGINE_VALU,
     SUPPORTED_HEAD_DIMS,
@@ -18,6 +19,7 @@ from .ops import (  # noqa: F401
 )
 
 __all__ = [
+    "BatchDecodeWrapper",
     "paged_attention_decode",
     "paged_attention_decode_cuda_v4",
     "paged_attention_decode_ex",

@@ -115,6 +115,24 @@ SIGNATURES = {
     ),
     "pad_decode_launch_noalloc": (
         [_VP, _VP, _VP, _VP, _VP, _VP, ctypes.POINTER(PadDims), ctypes.c_float, ctypes.c_int, _VP], ctypes.c_int),
+    "pad_decode_worklist_bytes": (
+        [ctypes.POINTER(PadDims), ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)],
+        ctypes.c_int,
+    ),
+    "pad_decode_plan_worklist": (
+        [_VP, _VP, ctypes.POINTER(PadDims), ctypes.c_int, _VP, ctypes.c_size_t, _VP], ctypes.c_int),
+    "pad_decode_plan_worklist_csr": (
+        [_VP, _VP, _VP, ctypes.POINTER(PadDims), ctypes.c_int, _VP, ctypes.c_size_t, _VP], ctypes.c_int),
+    "pad_decode_launch_worklist": (
+        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, _VP, ctypes.c_int64, ctypes.POINTER(PadDims),
+         ctypes.c_float, ctypes.c_int, _VP, ctypes.c_size_t, _VP],
+        ctypes.c_int,
+    ),
+    "pad_decode_launch_worklist_csr": (
+        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, _VP, ctypes.c_int64, ctypes.POINTER(PadDims),
+         ctypes.c_float, ctypes.c_int, _VP, ctypes.c_size_t, _VP],
+        ctypes.c_int,
+    ),
     "pad_device_num_cus": ([ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "pad_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "pad_decode_abi_version": ([], ctypes.c_int),

@@ -118,11 +118,13 @@ struct Phase1Args {
                    //    unit when every sequence is full)
   int min_chunk;   // planner: fewest pages per item
   int pair_heads;  // 1: workgroups 8 apart take kv heads 2m and 2m+1 (see grid_pos)
+  int wl_key;      // key of the launch's plan, matched against the work list's header
   float scale_log2;
   const int32_t* bt;      // dense: block_table [B, max_pages]; CSR: indices
   const int32_t* sl;      // dense: seq_lens [B]
   const int32_t* indptr;  // CSR: [B + 1] offsets of each sequence's page ids in bt
   const int32_t* lpl;     // CSR: [B] tokens in each sequence's last page
+  const int32_t* worklist;  // precomputed work items (header + one record per workgroup) or nullptr
   int64_t sbb, sbp;
   int64_t ssl;
   const _Float16* q;
@@ -1171,6 +1173,71 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int
   return plan_item<NK>(a, t, g, G, lane);
 }
 
+// The work item of workgroup (s, h, bz) = slot g: the in-kernel plan when
+// a.balance is set, else the static split.  static_len is seq_lens[bz]
+// (dense) or any word (CSR).  The decode kernel and the work-list planner
+// both call this, so a planned launch runs exactly the items of an
+// unplanned one.
+__device__ __forceinline__ WorkItem resolve_workgroup(const Phase1Args& a, int s, int h, int bz, int g, int G,
+                                                      int lin, const int32_t* static_row, int static_len,
+                                                      int lane) {
+  if (a.balance) {
+    if (a.batch <= 64) return resolve_item<1>(a, s, h, bz, g, G, lin, static_row, lane);
+    return resolve_item<4>(a, s, h, bz, g, G, lin, static_row, lane);
+  }
+  if (a.csr) {
+    int row, pages, L;
+    csr_row(a, bz, &row, &pages, &L);
+    return static_item(a, s, h, bz, L, pages, a.bt + row, 1);
+  }
+  const int L = max(static_len, 0);
+  return static_item(a, s, h, bz, L, min(pages_for(a, L), a.max_pages), static_row, a.sbp);
+}
+
+// Work list (pad_decode_plan_worklist): a header of kWlHeaderInts int32
+// {magic, plan key, G} and one record of kWlRecordInts int32 per workgroup
+// slot g: {b, kvh, p_begin, p_end, L, nsplit, slot0, col_max, valid, row
+// (CSR offset of the sequence's ids, else 0), 6 unused, then the raw page id
+// of the first block of waves 0-7 (whole-page blocks; 0 otherwise), 8
+// unused}.
+constexpr int kWlHeaderInts = 32;
+constexpr int kWlRecordInts = 32;
+constexpr int kWlMagic = 0x574c4150;  // "PALW"
+
+// Record g of a.worklist as a work item and the raw first page id of this
+// wave's first block.  False (use the in-kernel plan) when the header does
+// not carry this launch's plan key.  A record that does not describe an
+// item of this launch's shapes is treated as no item, so a stale list can
+// give wrong rows but never reads or writes out of bounds.
+__device__ __forceinline__ bool worklist_item(const Phase1Args& a, int g, int G, int wave, WorkItem& w, int& pid) {
+  const int32_t* r = a.worklist + kWlHeaderInts + (int64_t)kWlRecordInts * g;
+  const int magic = load_uniform_i32(a.worklist);
+  const int key = load_uniform_i32(a.worklist + 1);
+  int f[10];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) f[i] = load_uniform_i32(r + i);
+  pid = load_uniform_i32(r + 16 + wave);
+  if (magic != kWlMagic || key != a.wl_key) return false;
+  w.b = f[0];
+  w.kvh = f[1];
+  w.p_begin = f[2];
+  w.p_end = f[3];
+  w.L = f[4];
+  w.nsplit = f[5];
+  w.slot0 = f[6];
+  w.col_max = f[7];
+  const int row = f[9];
+  const bool ok = f[8] != 0 && w.b >= 0 && w.b < a.batch && w.kvh >= 0 && w.kvh < a.hkv && w.p_begin >= 0 &&
+                  w.p_begin <= w.p_end && w.p_end <= w.col_max + 1 && w.L >= 0 && w.nsplit >= 0 &&
+                  w.nsplit <= G && w.slot0 >= 0 && w.slot0 <= G - w.nsplit &&
+                  (w.nsplit == 0 || (g >= w.slot0 && g < w.slot0 + w.nsplit)) && row >= 0 &&
+                  (int64_t)row + w.col_max < a.max_pages;
+  w.valid = ok ? 1 : 0;
+  w.ids_row = a.csr ? a.bt + row : a.bt + (int64_t)(ok ? w.b : 0) * a.sbb;
+  w.ids_stride = a.csr ? 1 : a.sbp;
+  return true;
+}
+
 // Minimum waves per SIMD each phase-1 instantiation is compiled for (it
 // caps the registers per lane at 512 / waves).  The generic page-size mode
 // of head_dim 128 gets 2 (256 registers): its six prefetched page ids did
@@ -1209,6 +1276,45 @@ __device__ __forceinline__ void grid_pos(const Phase1Args& a, int& s, int& h, in
   }
 }
 
+// Work-list planner: one wave per workgroup slot of the decode grid, run
+// once per decode step (the sequence lengths and page ids it reads must not
+// change before the launches that use the list).  Lane i < 32 writes word i
+// of the record; slot 0 also writes the header.
+__global__ __launch_bounds__(64) void pad_plan_kernel(const Phase1Args a, int32_t* wl) {
+  int s, h, bz, lin;
+  grid_pos(a, s, h, bz, lin);
+  const int lane = threadIdx.x;
+  const int g = s + a.num_splits * (h + a.hkv * bz);
+  const int G = a.num_splits * a.hkv * a.batch;
+  const int32_t* static_row = a.bt + (int64_t)bz * a.sbb;
+  const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)bz * a.ssl);
+  const WorkItem it = resolve_workgroup(a, s, h, bz, g, G, lin, static_row, static_len, lane);
+  int v = 0;
+  switch (lane) {
+    case 0: v = it.b; break;
+    case 1: v = it.kvh; break;
+    case 2: v = it.p_begin; break;
+    case 3: v = it.p_end; break;
+    case 4: v = it.L; break;
+    case 5: v = it.nsplit; break;
+    case 6: v = it.slot0; break;
+    case 7: v = it.col_max; break;
+    case 8: v = it.valid; break;
+    case 9: v = a.csr ? (int)(it.ids_row - a.bt) : 0; break;
+    default: break;
+  }
+  // The first page id of wave w's first block, as the decode kernel's
+  // first_page_id() reads it (whole-page blocks only).
+  const int w = lane - 16;
+  if (w >= 0 && w < a.nw && it.valid && it.col_max >= 0 && a.ps % kBlockTokens == 0) {
+    const int col = min(it.p_begin + block_page(a, w), it.col_max);
+    v = it.ids_row[(int64_t)col * it.ids_stride];
+  }
+  int32_t* r = wl + kWlHeaderInts + (int64_t)kWlRecordInts * g;
+  if (lane < kWlRecordInts) r[lane] = v;
+  if (g == 0 && lane < 3) wl[lane] = lane == 0 ? kWlMagic : (lane == 1 ? a.wl_key : G);
+}
+
 // Phase 1: one workgroup per (split, kv head, sequence).
 template <int D, int MODE, int ENGINE, int GQA_T>
 __global__ __launch_bounds__(max_group_waves(D) * 64)
@@ -1239,30 +1345,25 @@ void pad_phase1_kernel(const Phase1Args a) {
   const int g = s + a.num_splits * (h + a.hkv * bz);
   const int G = a.num_splits * a.hkv * a.batch;
 
-  // Dense page table: read the first page id of this workgroup's static
-  // split before the sequence lengths arrive; it stays valid whenever the
-  // item turns out to be the static one.
-  const int32_t* static_row = a.bt + (int64_t)bz * a.sbb;
-  int phys_first = 0;
-  if constexpr (ENGINE == 0 && MODE == kModeUniform) {
-    if (!a.csr) phys_first = first_page_id(a, static_row, a.sbp, a.max_pages - 1, s * a.pps, wave);
-  }
-  // Read unconditionally (any valid word when unused) after the page id, so
-  // both reads share one round trip.
-  const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)bz * a.ssl);
+  // With a work list, the item and its first page ids arrive in one round
+  // trip.  Otherwise, with the dense table, read the first page id of this
+  // workgroup's static split before the sequence lengths arrive; it stays
+  // valid whenever the item turns out to be the static one.
   WorkItem it;
-  if (a.balance) {
-    if (a.batch <= 64)
-      it = resolve_item<1>(a, s, h, bz, g, G, lin, static_row, lane);
-    else
-      it = resolve_item<4>(a, s, h, bz, g, G, lin, static_row, lane);
-  } else if (a.csr) {
-    int row, pages, L;
-    csr_row(a, bz, &row, &pages, &L);
-    it = static_item(a, s, h, bz, L, pages, a.bt + row, 1);
+  int phys_first = 0;
+  bool first_known;
+  if (a.worklist != nullptr && worklist_item(a, g, G, wave, it, phys_first)) {
+    first_known = true;
   } else {
-    const int L = max(static_len, 0);
-    it = static_item(a, s, h, bz, L, min(pages_for(a, L), a.max_pages), static_row, a.sbp);
+    const int32_t* static_row = a.bt + (int64_t)bz * a.sbb;
+    if constexpr (ENGINE == 0 && MODE == kModeUniform) {
+      if (!a.csr) phys_first = first_page_id(a, static_row, a.sbp, a.max_pages - 1, s * a.pps, wave);
+    }
+    // Read unconditionally (any valid word when unused) after the page id, so
+    // both reads share one round trip.
+    const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)bz * a.ssl);
+    it = resolve_workgroup(a, s, h, bz, g, G, lin, static_row, static_len, lane);
+    first_known = !a.csr && it.b == bz && it.p_begin == s * a.pps;
   }
   PAD_TL(lin, PAD_TL_ITEM);
   if (!it.valid) {
@@ -1286,8 +1387,7 @@ void pad_phase1_kernel(const Phase1Args a) {
     return;
   }
   if constexpr (ENGINE == 0 && MODE == kModeUniform) {
-    if (a.csr || b != bz || it.p_begin != s * a.pps)
-      phys_first = first_page_id(a, it.ids_row, it.ids_stride, it.col_max, it.p_begin, wave);
+    if (!first_known) phys_first = first_page_id(a, it.ids_row, it.ids_stride, it.col_max, it.p_begin, wave);
   }
   const int t_begin = it.p_begin * a.ps;
   const int t_end = min(it.p_end * a.ps, it.L);
@@ -1686,13 +1786,37 @@ static hipError_t dispatch_phase1(const Phase1Args& a, dim3 grid, int nw, size_t
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Everything one decode launch needs: kernel arguments, plan, grid, LDS.
+struct Launch {
+  Phase1Args a;
+  pad_decode_plan_t plan;
+  dim3 grid;
+  int nw;
+  size_t lds;
+  bool empty;  // batch 0: nothing to launch
+};
+
+// Key of a launch's plan, stored in a work list's header: the fields that
+// decide the grid and which item each workgroup gets (FNV-1a).
+static int plan_key(const Phase1Args& a) {
+  const int f[] = {a.batch, a.hkv, a.max_pages, a.num_splits, a.nw, a.csr, a.balance,
+                   a.ps, a.pps, a.gqa, a.pair_heads, a.min_chunk};
+  uint32_t h = 2166136261u;
+  for (int x : f) {
+    h ^= (uint32_t)x;
+    h *= 16777619u;
+  }
+  return (int)(h & 0x7fffffff);
+}
+
 // Dense page table: bt = block_table, sl = seq_lens, indptr = lpl = NULL.
 // CSR: bt = indices, indptr / lpl given, sl unused (dims->max_pages is the
-// number of entries in indices).
-static int launch_impl(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
-                       const int32_t* indptr, const int32_t* lpl, void* out, void* ws, size_t ws_bytes,
-                       int32_t* counters, int64_t num_counters, const pad_decode_dims* d, float scale,
-                       int num_splits, int engine, void* const* events, void* stream) {
+// number of entries in indices).  io: also check q/k/v/out and the scratch
+// (a work-list plan reads only the index arrays).
+static int setup_launch(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
+                        const int32_t* indptr, const int32_t* lpl, void* out, void* ws, size_t ws_bytes,
+                        int32_t* counters, int64_t num_counters, const pad_decode_dims* d, float scale,
+                        int num_splits, int engine, bool io, Launch* L) {
   if (engine != 0 && engine != 1) return PAD_ERR_INVALID_SHAPE;
   // Page ids are bounds-checked against num_pages on the device (an id
   // outside [0, num_pages) reads page 0), so a launch that reads pages needs
@@ -1702,30 +1826,32 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   int st = device_cus(&cus);
   if (st != PAD_OK) return st;
   const bool csr = indptr != nullptr || lpl != nullptr;
-  pad_decode_plan_t plan;
+  pad_decode_plan_t& plan = L->plan;
   st = plan_impl(d, num_splits, cus, engine, csr, &plan);
   if (st != PAD_OK) return st;
   const int gqa = d->num_q_heads / d->num_kv_heads;
   if (engine == 1 && !valu_supported(d->head_dim, gqa)) return PAD_ERR_UNSUPPORTED_GQA;
-  if (d->batch == 0) return PAD_OK;
-  if (!q || !k || !v || !out) return PAD_ERR_NULL_POINTER;
+  L->empty = d->batch == 0;
+  if (L->empty) return PAD_OK;
   if (csr ? (!indptr || !lpl || (!bt && d->max_pages > 0)) : (!bt || !sl)) return PAD_ERR_NULL_POINTER;
-  // 16-byte rows: every K/V/q/out row start must be 16-byte aligned.
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return PAD_ERR_ALIGNMENT;
-  if ((d->q_stride[0] | d->q_stride[1]) % 8 || (d->out_stride[0] | d->out_stride[1]) % 8 ||
-      (d->k_stride[0] | d->k_stride[1] | d->k_stride[2]) % 8 ||
-      (d->v_stride[0] | d->v_stride[1] | d->v_stride[2]) % 8)
-    return PAD_ERR_ALIGNMENT;
-  if (!plan.single_pass && (!ws || ws_bytes < plan.workspace_bytes)) return PAD_ERR_WORKSPACE;
-  if (!plan.single_pass && (!counters || num_counters < plan.counters)) return PAD_ERR_WORKSPACE;
+  if (io) {
+    if (!q || !k || !v || !out) return PAD_ERR_NULL_POINTER;
+    // 16-byte rows: every K/V/q/out row start must be 16-byte aligned.
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out)) return PAD_ERR_ALIGNMENT;
+    if ((d->q_stride[0] | d->q_stride[1]) % 8 || (d->out_stride[0] | d->out_stride[1]) % 8 ||
+        (d->k_stride[0] | d->k_stride[1] | d->k_stride[2]) % 8 ||
+        (d->v_stride[0] | d->v_stride[1] | d->v_stride[2]) % 8)
+      return PAD_ERR_ALIGNMENT;
+    if (!plan.single_pass && (!ws || ws_bytes < plan.workspace_bytes)) return PAD_ERR_WORKSPACE;
+    if (!plan.single_pass && (!counters || num_counters < plan.counters)) return PAD_ERR_WORKSPACE;
+  }
 
-  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   const int S = plan.num_splits;
   float* o_part = nullptr;
   float2* ml_part = nullptr;
-  if (!plan.single_pass) workspace_layout(d, S, ws, &o_part, &ml_part);
+  if (io && !plan.single_pass) workspace_layout(d, S, ws, &o_part, &ml_part);
 
-  Phase1Args a;
+  Phase1Args& a = L->a;
   a.q = static_cast<const _Float16*>(q);
   a.k = static_cast<const _Float16*>(k);
   a.v = static_cast<const _Float16*>(v);
@@ -1733,6 +1859,7 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   a.sl = sl;
   a.indptr = indptr;
   a.lpl = lpl;
+  a.worklist = nullptr;
   a.out = static_cast<_Float16*>(out);
   a.o_part = o_part;
   a.ml_part = ml_part;
@@ -1772,23 +1899,48 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
     if ((1 << sh) == d->page_size) a.ps_shift = sh;
   a.scale_log2 = scale * kLog2e;
   a.nw = plan.waves_per_group;
+  a.wl_key = plan_key(a);
 #ifdef PAD_TIMELINE
-  a.tl_launch = tl_launches++ % PAD_TL_LAUNCHES;
+  a.tl_launch = 0;
 #endif
+  L->nw = plan.waves_per_group;
+  L->lds = group_lds_bytes(L->nw, gqa, d->head_dim, engine);
+  L->grid = dim3(S, d->num_kv_heads, d->batch);
+  return PAD_OK;
+}
 
-  const int nw = plan.waves_per_group;
-  const size_t lds = group_lds_bytes(nw, gqa, d->head_dim, engine);
-  const dim3 grid1(S, d->num_kv_heads, d->batch);
+// Bytes of the work list of this plan: header plus one record per workgroup.
+static size_t worklist_bytes_for(const pad_decode_plan_t& plan, const pad_decode_dims* d) {
+  const int64_t G = (int64_t)plan.num_splits * d->num_kv_heads * d->batch;
+  return sizeof(int32_t) * (size_t)(kWlHeaderInts + kWlRecordInts * G);
+}
 
+static int launch_impl(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
+                       const int32_t* indptr, const int32_t* lpl, void* out, void* ws, size_t ws_bytes,
+                       int32_t* counters, int64_t num_counters, const pad_decode_dims* d, float scale,
+                       int num_splits, int engine, void* const* events, void* stream,
+                       const void* worklist = nullptr, size_t worklist_bytes = 0) {
+  Launch L;
+  int st = setup_launch(q, k, v, bt, sl, indptr, lpl, out, ws, ws_bytes, counters, num_counters, d, scale,
+                        num_splits, engine, true, &L);
+  if (st != PAD_OK || L.empty) return st;
+  if (worklist != nullptr) {
+    if (worklist_bytes < worklist_bytes_for(L.plan, d)) return PAD_ERR_WORKSPACE;
+    L.a.worklist = static_cast<const int32_t*>(worklist);
+  }
+#ifdef PAD_TIMELINE
+  L.a.tl_launch = tl_launches++ % PAD_TL_LAUNCHES;
+#endif
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   if (events && events[0] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[0]), hs) != hipSuccess)
     return PAD_ERR_LAUNCH;
   hipError_t e;
   switch (d->head_dim) {
-    case 32: e = dispatch_phase1<32>(a, grid1, nw, lds, engine, hs); break;
-    case 64: e = dispatch_phase1<64>(a, grid1, nw, lds, engine, hs); break;
-    case 96: e = dispatch_phase1<96>(a, grid1, nw, lds, engine, hs); break;
-    case 128: e = dispatch_phase1<128>(a, grid1, nw, lds, engine, hs); break;
-    default: e = dispatch_phase1<256>(a, grid1, nw, lds, engine, hs); break;
+    case 32: e = dispatch_phase1<32>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
+    case 64: e = dispatch_phase1<64>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
+    case 96: e = dispatch_phase1<96>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
+    case 128: e = dispatch_phase1<128>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
+    default: e = dispatch_phase1<256>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
   }
   if (e != hipSuccess) return PAD_ERR_LAUNCH;
   if (events && events[1] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[1]), hs) != hipSuccess)
@@ -1796,6 +1948,23 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   if (events && events[2] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[2]), hs) != hipSuccess)
     return PAD_ERR_LAUNCH;
   return PAD_OK;
+}
+
+// Writes the work list of a launch with these dims and indices (one wave per
+// workgroup slot of the decode grid).
+static int plan_worklist_impl(const int32_t* bt, const int32_t* sl, const int32_t* indptr, const int32_t* lpl,
+                              const pad_decode_dims* d, int num_splits, void* worklist, size_t worklist_bytes,
+                              void* stream) {
+  Launch L;
+  int st = setup_launch(nullptr, nullptr, nullptr, bt, sl, indptr, lpl, nullptr, nullptr, 0, nullptr, 0, d, 1.0f,
+                        num_splits, 0, false, &L);
+  if (st != PAD_OK) return st;
+  if (!worklist) return PAD_ERR_NULL_POINTER;
+  if (worklist_bytes < worklist_bytes_for(L.plan, d)) return PAD_ERR_WORKSPACE;
+  if (L.empty) return PAD_OK;
+  hipLaunchKernelGGL(pad_plan_kernel, L.grid, dim3(64), 0, reinterpret_cast<hipStream_t>(stream), L.a,
+                     static_cast<int32_t*>(worklist));
+  return hipGetLastError() == hipSuccess ? PAD_OK : PAD_ERR_LAUNCH;
 }
 
 // ---------------------------------------------------------------------------
@@ -1924,6 +2093,50 @@ int pad_decode_launch_noalloc(const void* q, const void* k_cache, const void* v_
                               const int32_t* seq_lens, void* out, const pad_decode_dims* dims, float scale,
                               int num_splits, void* stream) {
   return pad::launch_noalloc(q, k_cache, v_cache, block_table, seq_lens, out, dims, scale, num_splits, stream);
+}
+
+int pad_decode_worklist_bytes(const pad_decode_dims* dims, int num_splits, int num_cus, int csr, size_t* bytes) {
+  if (!bytes) return PAD_ERR_NULL_POINTER;
+  pad_decode_plan_t p;
+  const int st = pad::plan_impl(dims, num_splits, num_cus, 0, csr != 0, &p);
+  if (st != PAD_OK) return st;
+  *bytes = pad::worklist_bytes_for(p, dims);
+  return PAD_OK;
+}
+
+int pad_decode_plan_worklist(const int32_t* block_table, const int32_t* seq_lens, const pad_decode_dims* dims,
+                             int num_splits, void* worklist, size_t worklist_bytes, void* stream) {
+  return pad::plan_worklist_impl(block_table, seq_lens, nullptr, nullptr, dims, num_splits, worklist, worklist_bytes,
+                                 stream);
+}
+
+int pad_decode_plan_worklist_csr(const int32_t* indices, const int32_t* indptr, const int32_t* last_page_len,
+                                 const pad_decode_dims* dims, int num_splits, void* worklist, size_t worklist_bytes,
+                                 void* stream) {
+  if (!indptr || !last_page_len) return PAD_ERR_NULL_POINTER;
+  return pad::plan_worklist_impl(indices, nullptr, indptr, last_page_len, dims, num_splits, worklist,
+                                 worklist_bytes, stream);
+}
+
+int pad_decode_launch_worklist(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                               const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
+                               int32_t* counters, int64_t num_counters, const pad_decode_dims* dims, float scale,
+                               int num_splits, const void* worklist, size_t worklist_bytes, void* stream) {
+  if (!worklist) return PAD_ERR_NULL_POINTER;
+  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, nullptr, nullptr, out, workspace,
+                          workspace_bytes, counters, num_counters, dims, scale, num_splits, 0, nullptr, stream,
+                          worklist, worklist_bytes);
+}
+
+int pad_decode_launch_worklist_csr(const void* q, const void* k_cache, const void* v_cache, const int32_t* indices,
+                                   const int32_t* indptr, const int32_t* last_page_len, void* out, void* workspace,
+                                   size_t workspace_bytes, int32_t* counters, int64_t num_counters,
+                                   const pad_decode_dims* dims, float scale, int num_splits, const void* worklist,
+                                   size_t worklist_bytes, void* stream) {
+  if (!indptr || !last_page_len || !worklist) return PAD_ERR_NULL_POINTER;
+  return pad::launch_impl(q, k_cache, v_cache, indices, nullptr, indptr, last_page_len, out, workspace,
+                          workspace_bytes, counters, num_counters, dims, scale, num_splits, 0, nullptr, stream,
+                          worklist, worklist_bytes);
 }
 
 int pad_decode_counters_init(int32_t* counters, int64_t num_counters, void* stream) {

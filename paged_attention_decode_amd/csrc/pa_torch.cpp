@@ -17,6 +17,9 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
+#include <climits>
+#include <cstdint>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -237,6 +240,191 @@ torch::Tensor forward_csr(torch::Tensor q, torch::Tensor k_cache, torch::Tensor 
   return out;
 }
 
+// Plan once, run many (pad_decode_plan_worklist / pad_decode_launch_worklist):
+// the dims of a decode with these index tensors and head/page geometry.
+// q/k/v/out strides do not enter the plan; num_pages only bounds page ids at
+// run time, so the plan uses any positive value.
+pad_decode_dims worklist_dims(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                              int64_t page_size, int64_t max_pages) {
+  pad_decode_dims d;
+  std::memset(&d, 0, sizeof(d));
+  d.batch = static_cast<int32_t>(batch);
+  d.num_q_heads = static_cast<int32_t>(num_q_heads);
+  d.num_kv_heads = static_cast<int32_t>(num_kv_heads);
+  d.head_dim = static_cast<int32_t>(head_dim);
+  d.page_size = static_cast<int32_t>(page_size);
+  d.max_pages = static_cast<int32_t>(max_pages);
+  d.num_pages = INT64_MAX;
+  d.q_stride[2] = d.k_stride[3] = d.v_stride[3] = d.out_stride[2] = 1;
+  return d;
+}
+
+torch::Tensor new_worklist(const torch::Tensor& like, const pad_decode_dims& d, int64_t num_splits, bool csr) {
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(like.device());
+  size_t bytes = 0;
+  const int st = pad_decode_worklist_bytes(&d, static_cast<int>(num_splits), cached_cus(like.get_device()),
+                                           csr ? 1 : 0, &bytes);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return torch::empty({static_cast<int64_t>(bytes)}, like.options().dtype(at::kByte));
+}
+
+// Work list of a dense-table decode (block_table [B, max_pages], seq_lens [B], int32 on the GPU).
+torch::Tensor plan_worklist(torch::Tensor block_table, torch::Tensor seq_lens, int64_t num_q_heads,
+                            int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_splits) {
+  TORCH_CHECK(block_table.is_cuda() && seq_lens.is_cuda() && block_table.device() == seq_lens.device(),
+              "pa_decode: block_table and seq_lens must be on the same GPU");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt && seq_lens.scalar_type() == at::kInt,
+              "pa_decode: block_table and seq_lens must be int32");
+  TORCH_CHECK(block_table.dim() == 2 && seq_lens.dim() == 1 && seq_lens.size(0) == block_table.size(0),
+              "pa_decode: block_table must be [batch, max_pages] and seq_lens [batch]");
+  pad_decode_dims d = worklist_dims(block_table.size(0), num_q_heads, num_kv_heads, head_dim, page_size,
+                                    block_table.size(1));
+  d.bt_stride[0] = block_table.stride(0);
+  d.bt_stride[1] = block_table.stride(1);
+  d.sl_stride = seq_lens.stride(0);
+  torch::Tensor wl = new_worklist(block_table, d, num_splits, false);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(block_table.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(block_table.get_device()).stream();
+  const int st = pad_decode_plan_worklist(block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), &d,
+                                          static_cast<int>(num_splits), wl.data_ptr(),
+                                          static_cast<size_t>(wl.numel()), stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return wl;
+}
+
+// Work list of a CSR decode (indptr [B + 1], indices [nnz], last_page_len [B], int32 on the GPU).
+torch::Tensor plan_worklist_csr(torch::Tensor indptr, torch::Tensor indices, torch::Tensor last_page_len,
+                                int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
+                                int64_t num_splits) {
+  TORCH_CHECK(indptr.is_cuda() && indices.is_cuda() && last_page_len.is_cuda() &&
+                  indptr.device() == indices.device() && indptr.device() == last_page_len.device(),
+              "pa_decode: indptr, indices and last_page_len must be on the same GPU");
+  TORCH_CHECK(indptr.scalar_type() == at::kInt && indices.scalar_type() == at::kInt &&
+                  last_page_len.scalar_type() == at::kInt,
+              "pa_decode: indptr, indices and last_page_len must be int32");
+  TORCH_CHECK(indptr.dim() == 1 && indices.dim() == 1 && last_page_len.dim() == 1 &&
+                  indptr.size(0) == last_page_len.size(0) + 1 && indptr.is_contiguous() &&
+                  indices.is_contiguous() && last_page_len.is_contiguous(),
+              "pa_decode: indptr [batch + 1], indices [nnz] and last_page_len [batch] must be contiguous");
+  TORCH_CHECK(indices.size(0) <= INT32_MAX, "pa_decode: too many page ids");
+  pad_decode_dims d = worklist_dims(last_page_len.size(0), num_q_heads, num_kv_heads, head_dim, page_size,
+                                    indices.size(0));
+  d.bt_stride[1] = 1;
+  torch::Tensor wl = new_worklist(indices, d, num_splits, true);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(indices.device());
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(indices.get_device()).stream();
+  const int st = pad_decode_plan_worklist_csr(indices.data_ptr<int32_t>(), indptr.data_ptr<int32_t>(),
+                                              last_page_len.data_ptr<int32_t>(), &d, static_cast<int>(num_splits),
+                                              wl.data_ptr(), static_cast<size_t>(wl.numel()), stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return wl;
+}
+
+// Decode from a work list (dense table): same arguments and result as
+// forward() with engine 0, plus the list plan_worklist() wrote for them.
+torch::Tensor forward_worklist(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                               torch::Tensor block_table, torch::Tensor seq_lens, torch::Tensor worklist,
+                               double scale, int64_t num_splits) {
+  TORCH_CHECK(worklist.is_cuda() && worklist.device() == q.device() && worklist.scalar_type() == at::kByte &&
+                  worklist.is_contiguous(),
+              "pa_decode: worklist must be a contiguous uint8 tensor on q's device");
+  TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && block_table.is_cuda() &&
+                  seq_lens.is_cuda(),
+              "pa_decode: all tensors must be on the GPU");
+  TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() &&
+                  q.device() == block_table.device() && q.device() == seq_lens.device(),
+              "pa_decode: all tensors must be on the same device");
+  TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
+                  v_cache.scalar_type() == at::kHalf,
+              "pa_decode: q, k_cache and v_cache must be float16");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt && seq_lens.scalar_type() == at::kInt,
+              "pa_decode: block_table and seq_lens must be int32");
+  TORCH_CHECK(q.dim() == 3 && k_cache.dim() == 4 && v_cache.sizes() == k_cache.sizes(),
+              "pa_decode: q must be [batch, num_q_heads, head_dim] and the caches 4-D and alike");
+  TORCH_CHECK(block_table.dim() == 2 && block_table.size(0) == q.size(0) && seq_lens.dim() == 1 &&
+                  seq_lens.size(0) == q.size(0),
+              "pa_decode: block_table must be [batch, max_pages] and seq_lens [batch]");
+  TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+  pad_decode_dims d;
+  fill_dims(q, k_cache, v_cache, block_table, seq_lens, out, &d);
+  pad_decode_plan_t plan;
+  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cached_cus(q.get_device()), &plan);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  void* ws_ptr = nullptr;
+  int32_t* counters = nullptr;
+  if (!plan.single_pass) {
+    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
+    ws_ptr = sc.workspace.data_ptr();
+    counters = sc.counters.data_ptr<int32_t>();
+  }
+  st = pad_decode_launch_worklist(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                  block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
+                                  ws_ptr, plan.workspace_bytes, counters, plan.counters, &d,
+                                  static_cast<float>(scale), static_cast<int>(num_splits), worklist.data_ptr(),
+                                  static_cast<size_t>(worklist.numel()), stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return out;
+}
+
+// Decode from a work list (CSR index): forward_csr() with engine 0 plus the
+// list plan_worklist_csr() wrote for the same index tensors.
+torch::Tensor forward_worklist_csr(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                                   torch::Tensor indptr, torch::Tensor indices, torch::Tensor last_page_len,
+                                   torch::Tensor worklist, double scale, int64_t num_splits) {
+  TORCH_CHECK(worklist.is_cuda() && worklist.device() == q.device() && worklist.scalar_type() == at::kByte &&
+                  worklist.is_contiguous(),
+              "pa_decode: worklist must be a contiguous uint8 tensor on q's device");
+  TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && indptr.is_cuda() && indices.is_cuda() &&
+                  last_page_len.is_cuda(),
+              "pa_decode: all tensors must be on the GPU");
+  TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() && q.device() == indptr.device() &&
+                  q.device() == indices.device() && q.device() == last_page_len.device(),
+              "pa_decode: all tensors must be on the same device");
+  TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
+                  v_cache.scalar_type() == at::kHalf,
+              "pa_decode: q, k_cache and v_cache must be float16");
+  TORCH_CHECK(indptr.scalar_type() == at::kInt && indices.scalar_type() == at::kInt &&
+                  last_page_len.scalar_type() == at::kInt,
+              "pa_decode: indptr, indices and last_page_len must be int32");
+  TORCH_CHECK(q.dim() == 3 && k_cache.dim() == 4 && v_cache.sizes() == k_cache.sizes(),
+              "pa_decode: q must be [batch, num_q_heads, head_dim] and the caches 4-D and alike");
+  TORCH_CHECK(indptr.dim() == 1 && indptr.size(0) == q.size(0) + 1 && last_page_len.dim() == 1 &&
+                  last_page_len.size(0) == q.size(0) && indices.dim() == 1 && indices.is_contiguous() &&
+                  indptr.is_contiguous() && last_page_len.is_contiguous(),
+              "pa_decode: indptr [batch + 1], indices [nnz] and last_page_len [batch] must be contiguous");
+  TORCH_CHECK(indices.size(0) <= INT32_MAX, "pa_decode: too many page ids");
+  TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+  pad_decode_dims d;
+  fill_dims(q, k_cache, v_cache, indices.view({1, -1}), last_page_len, out, &d);
+  d.max_pages = static_cast<int32_t>(indices.size(0));
+  d.bt_stride[0] = 0;
+  d.bt_stride[1] = 1;
+  pad_decode_plan_t plan;
+  int st = pad_decode_plan_csr(&d, static_cast<int>(num_splits), cached_cus(q.get_device()), &plan);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  void* ws_ptr = nullptr;
+  int32_t* counters = nullptr;
+  if (!plan.single_pass) {
+    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
+    ws_ptr = sc.workspace.data_ptr();
+    counters = sc.counters.data_ptr<int32_t>();
+  }
+  st = pad_decode_launch_worklist_csr(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                      indices.data_ptr<int32_t>(), indptr.data_ptr<int32_t>(),
+                                      last_page_len.data_ptr<int32_t>(), out.data_ptr(), ws_ptr,
+                                      plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
+                                      static_cast<int>(num_splits), worklist.data_ptr(),
+                                      static_cast<size_t>(worklist.numel()), stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return out;
+}
+
 // Same argument list as the reference's forward_v4 binding
 // (cuda/kernels.h:60-70): gqa_ratio, head_dim and page_size must agree with
 // the tensor shapes.
@@ -292,5 +480,16 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Paged-attention decode over a CSR page index (q, k_cache, v_cache, indptr, indices, last_page_len, "
         "scale, num_splits, engine) -> out");
   m.def("plan", &plan, "Split plan for the given shapes (host only)");
+  m.def("plan_worklist", &plan_worklist,
+        "Work list of a dense-table decode (block_table, seq_lens, num_q_heads, num_kv_heads, head_dim, "
+        "page_size, num_splits) -> uint8 tensor");
+  m.def("plan_worklist_csr", &plan_worklist_csr,
+        "Work list of a CSR decode (indptr, indices, last_page_len, num_q_heads, num_kv_heads, head_dim, "
+        "page_size, num_splits) -> uint8 tensor");
+  m.def("forward_worklist", &forward_worklist,
+        "Decode from a work list (q, k_cache, v_cache, block_table, seq_lens, worklist, scale, num_splits) -> out");
+  m.def("forward_worklist_csr", &forward_worklist_csr,
+        "Decode from a work list (q, k_cache, v_cache, indptr, indices, last_page_len, worklist, scale, "
+        "num_splits) -> out");
   m.def("abi_version", &pad_decode_abi_version, "C ABI version of the linked libpa_decode.so");
 }

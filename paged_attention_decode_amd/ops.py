@@ -165,3 +165,106 @@ def plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_s
     entries (all sequences' pages)."""
     return ext().plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, num_splits, num_cus,
                       bool(csr))
+
+
+class BatchDecodeWrapper:
+    """Plan once per decode step, run once per layer.
+
+    The split the reference's FlashInfer adapter drives
+    (``BatchDecodeWithPagedKVCacheWrapper``: ``plan(indptr, indices,
+    last_page_len, num_qo_heads, num_kv_heads, head_dim, page_size, ...)``
+    then ``run(q, (k_cache, v_cache))``, src/flashinfer_adapter.py:100-112;
+    plan-once-run-many in bench/bench_flashinfer.py:131-151).  ``plan()``
+    queues one small kernel that writes the launch's work list: for every
+    workgroup of the decode grid, the (sequence, kv head) unit and page range
+    it processes and the page ids its waves read first.  ``run()`` decodes
+    from that list instead of working it out from the sequence lengths at
+    the start of every launch, and returns exactly what
+    :func:`paged_attention_decode_csr` (or, after :meth:`plan_block_table`,
+    :func:`paged_attention_decode`) returns for the same arguments.
+
+    The list encodes the lengths and page ids: plan again when they change
+    (in a decoding loop, once per step, before the first layer).  The index
+    tensors given to ``plan()`` are kept and read again by every ``run()``.
+    """
+
+    def __init__(self):
+        self._plan = None
+
+    def plan(self, indptr, indices, last_page_len, num_qo_heads, num_kv_heads, head_dim, page_size,
+             sm_scale=None, num_splits=None):
+        """Plan over a CSR page index (FlashInfer's layout, see :func:`paged_kv_indices`)."""
+        assert indptr.is_cuda and indices.is_cuda and last_page_len.is_cuda, "CSR index tensors must be GPU tensors"
+        assert indptr.dim() == 1 and last_page_len.dim() == 1 and indptr.shape[0] == last_page_len.shape[0] + 1, (
+            "indptr must be [batch + 1] and last_page_len [batch]"
+        )
+        assert indices.dim() == 1, "indices must be 1-D"
+        self._check_geometry(num_qo_heads, num_kv_heads, head_dim, page_size)
+        indptr = indptr.to(torch.int32).contiguous()
+        indices = indices.to(torch.int32).contiguous()
+        last_page_len = last_page_len.to(torch.int32).contiguous()
+        splits = self._splits(num_splits)
+        wl = ext().plan_worklist_csr(indptr, indices, last_page_len, num_qo_heads, num_kv_heads, head_dim,
+                                     page_size, splits)
+        self._plan = ("csr", (indptr, indices, last_page_len), wl, splits,
+                      (int(last_page_len.shape[0]), num_qo_heads, num_kv_heads, head_dim, page_size),
+                      self._scale(sm_scale, head_dim))
+
+    def plan_block_table(self, block_table, seq_lens, num_qo_heads, num_kv_heads, head_dim, page_size,
+                         sm_scale=None, num_splits=None):
+        """Plan over the reference's dense ``block_table [B, max_pages]`` and ``seq_lens [B]``."""
+        assert block_table.is_cuda and seq_lens.is_cuda, "block_table and seq_lens must be GPU tensors"
+        assert block_table.dim() == 2 and seq_lens.dim() == 1 and block_table.shape[0] == seq_lens.shape[0], (
+            "block_table must be [batch, max_pages] and seq_lens [batch]"
+        )
+        self._check_geometry(num_qo_heads, num_kv_heads, head_dim, page_size)
+        if block_table.dtype != torch.int32:
+            block_table = block_table.to(torch.int32)
+        if seq_lens.dtype != torch.int32:
+            seq_lens = seq_lens.to(torch.int32)
+        splits = self._splits(num_splits)
+        wl = ext().plan_worklist(block_table, seq_lens, num_qo_heads, num_kv_heads, head_dim, page_size, splits)
+        self._plan = ("dense", (block_table, seq_lens), wl, splits,
+                      (int(seq_lens.shape[0]), num_qo_heads, num_kv_heads, head_dim, page_size),
+                      self._scale(sm_scale, head_dim))
+
+    def run(self, q, paged_kv_cache):
+        """Decode ``q [batch, num_qo_heads, head_dim]`` against ``(k_cache, v_cache)``; fp16 shaped like q."""
+        assert self._plan is not None, "call plan() or plan_block_table() before run()"
+        kind, index, wl, splits, geometry, scale = self._plan
+        k_cache, v_cache = paged_kv_cache
+        assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "paged_attention_decode requires GPU tensors"
+        assert q.dtype == torch.float16 and k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16, (
+            "paged_attention_decode expects fp16 q/k_cache/v_cache"
+        )
+        assert q.dim() == 3 and k_cache.dim() == 4 and v_cache.shape == k_cache.shape, "bad q / cache shapes"
+        batch, num_qo_heads, num_kv_heads, head_dim, page_size = geometry
+        assert tuple(q.shape) == (batch, num_qo_heads, head_dim), "q does not match the planned shapes"
+        assert k_cache.shape[1] == page_size and k_cache.shape[2] == num_kv_heads and k_cache.shape[3] == head_dim, (
+            "k_cache does not match the planned page size / heads / head_dim"
+        )
+        assert k_cache.stride(3) == 1 and v_cache.stride(3) == 1, "K/V caches need a contiguous head_dim"
+        if kind == "csr":
+            return ext().forward_worklist_csr(_aligned_q(q), k_cache, v_cache, *index, wl, scale, splits)
+        return ext().forward_worklist(_aligned_q(q), k_cache, v_cache, *index, wl, scale, splits)
+
+    @staticmethod
+    def _check_geometry(num_qo_heads, num_kv_heads, head_dim, page_size):
+        assert num_kv_heads > 0 and num_qo_heads % num_kv_heads == 0, (
+            "num_qo_heads must be divisible by num_kv_heads (GQA)"
+        )
+        assert num_qo_heads // num_kv_heads <= MAX_GQA, f"GQA group larger than {MAX_GQA}"
+        assert head_dim in SUPPORTED_HEAD_DIMS, f"head_dim must be one of {SUPPORTED_HEAD_DIMS}"
+        assert page_size >= 1, "page_size must be >= 1"
+
+    @staticmethod
+    def _splits(num_splits):
+        if num_splits is None:
+            return 0
+        num_splits = int(num_splits)
+        assert num_splits >= 1, "num_splits must be >= 1"
+        return num_splits
+
+    @staticmethod
+    def _scale(sm_scale, head_dim):
+        return float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(head_dim)

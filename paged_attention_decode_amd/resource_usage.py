@@ -65,7 +65,7 @@ def table(rows: list[dict]) -> str:
     out = [f"{'kernel':22s} {'template':18s} {'VGPR':>4s} {'AGPR':>4s} {'SGPR':>4s} {'scratch':>7s} "
            f"{'sgpr_spill':>10s} {'vgpr_spill':>10s} {'waves/SIMD':>10s} {'LDS':>5s}"]
     for r in rows:
-        kern = next((k for k in ("pad_phase1_kernel", "pad_zero_i32_kernel") if k in r["name"]), r["name"][:22])
+        kern = next((k for k in ("pad_phase1_kernel", "pad_plan_kernel", "pad_zero_i32_kernel") if k in r["name"]), r["name"][:22])
         tmpl = r["template"] if r["template"].startswith("<") else "-"
         out.append(f"{kern:22s} {tmpl:18s} {r.get('vgpr', 0):4d} {r.get('agpr', 0):4d} "
                    f"{r.get('sgpr', 0):4d} {r.get('scratch', 0):7d} {r.get('sgpr_spill', 0):10d} "

@@ -51,7 +51,7 @@ def test_library_exports_every_declared_symbol():
     lib = _native.capi()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.pad_decode_abi_version() == 3
+    assert lib.pad_decode_abi_version() == 4
 
 
 def test_status_strings():
