@@ -44,8 +44,15 @@ What one run measures (one GPU; ``--gpus`` above 1 exits with a message):
   arithmetic; libpa_probe.so via roofline.ceilings) reaches on the same
   rotated inputs - the practical ceiling for this page layout.
 * ``c3_ragged``: configuration C3 (batch 32, seq_lens uniform in
-  [1, 8192], page 32) through the drop-in (in-kernel planned splits) and
-  through the CSR page-index entry, cold throughput.
+  [1, 8192], page 32) through the drop-in (in-kernel planned splits),
+  through the CSR page-index entry, and planned once with
+  ``BatchDecodeWrapper`` then run (``*_planned``: the plan-once-run-many
+  flow of the reference's FlashInfer benchmark,
+  bench/bench_flashinfer.py:131-151 of the reference; the plan is made
+  before the timed region, as a decoding loop makes it once per step for
+  all layers), cold throughput.
+* ``c2_sweep[b].us_per_call_cold_planned``: the same plan-once-run-many
+  timing for each batch of C2.
 """
 
 from __future__ import annotations
@@ -113,6 +120,34 @@ def _throughput(pad, sets, engine, splits, steps, warmup):
     start.record()
     for i in range(steps):
         _call(pad, sets[i % len(sets)], engine, splits)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps
+
+
+def _throughput_planned(pad, sets, splits, steps, warmup):
+    """Seconds per call of BatchDecodeWrapper.run over `steps` back-to-back calls.
+
+    Each input set is planned once before the timed region (plan once per
+    decode step, run once per layer); the timed calls only run."""
+    import torch
+
+    wraps = []
+    for w in sets:
+        pw = pad.BatchDecodeWrapper()
+        sh = w.shape
+        pw.plan_block_table(w.block_table, w.seq_lens, sh["num_q_heads"], sh["num_kv_heads"], sh["head_dim"],
+                            sh["page_size"], num_splits=splits or None)
+        wraps.append(pw)
+    for i in range(warmup):
+        j = i % len(sets)
+        wraps[j].run(sets[j].q, (sets[j].k_cache, sets[j].v_cache))
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        j = i % len(sets)
+        wraps[j].run(sets[j].q, (sets[j].k_cache, sets[j].v_cache))
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / 1e3 / steps
@@ -371,6 +406,7 @@ def main():
         torch.cuda.synchronize()
         csr = s_ev.elapsed_time(e_ev) / 1e3 / calls
         nb3 = sum(wl.bytes_of(w) for w in rs) / len(rs)
+        planned = _throughput_planned(pad, rs, splits, calls, 20) if engine == 0 else None
         result["c3_ragged"] = {
             "workload": "C3: batch 32, seq_lens U[1, 8192], GQA 12/2, head_dim 128, page 32; cold "
                         f"(rotation over {len(rs)} seeded batches)",
@@ -380,6 +416,12 @@ def main():
             "us_per_call_csr": round(csr * 1e6, 2),
             "gbs_csr": round(nb3 / csr / 1e9, 1),
         }
+        if planned:
+            result["c3_ragged"].update({
+                "us_per_call_planned": round(planned * 1e6, 2),
+                "gbs_planned": round(nb3 / planned / 1e9, 1),
+                "pct_of_peak_planned": round(100 * nb3 / planned / 1e9 / PEAK_GBS, 2),
+            })
         del rs, csr_args
 
     if not args.no_sweep:
@@ -396,6 +438,10 @@ def main():
                 "gbs_cold": round(nb / cold / 1e9, 1),
                 "pct_of_peak_cold": round(100 * nb / cold / 1e9 / PEAK_GBS, 2),
             }
+            if engine == 0:
+                cold_p = _throughput_planned(pad, rs, splits, args.sweep_calls, 20)
+                sweep[str(b)]["us_per_call_cold_planned"] = round(cold_p * 1e6, 2)
+                sweep[str(b)]["pct_of_peak_cold_planned"] = round(100 * nb / cold_p / 1e9 / PEAK_GBS, 2)
             del rs, w
         result["c2_sweep"] = sweep
 

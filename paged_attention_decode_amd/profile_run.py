@@ -12,6 +12,10 @@ decode calls of the named configuration, rotating over enough distinct KV
 caches that the 256 MB Infinity Cache cannot serve repeats ("cold"), or on
 one set of inputs with ``--warm``.  Prints the per-call algorithmic bytes.
 
+``--planned`` plans every input set once with ``BatchDecodeWrapper``
+(the work-list planner kernel, one dispatch per set, before the timed
+calls) and then makes the ``--calls`` decode calls through ``run()``.
+
 ``--timeline`` instead runs each configuration of ``--configs`` (e.g.
 ``C2:16,C2:32,C3``) through ``libpa_decode_tl.so`` (the decode library with
 per-workgroup phase stamps) in groups of 4 back-to-back cold launches and
@@ -78,6 +82,8 @@ def main() -> None:
     p.add_argument("--configs", default="C2:16,C2:32,C2:64,C3,C4", help="--timeline: configurations")
     p.add_argument("--repeats", type=int, default=8, help="--timeline: groups of 4 launches")
     p.add_argument("--json", default="", help="--timeline: write the table here")
+    p.add_argument("--planned", action="store_true",
+                   help="plan every input set once (BatchDecodeWrapper), then time only run() calls")
     a = p.parse_args()
     if a.timeline:
         run_timeline(a)
@@ -106,10 +112,23 @@ def main() -> None:
             return wl.make(a.config, batch=a.batch, seed=seed)
     sets = _sets(make, a.warm)
     w0, n_sets = sets[0], len(sets)
+    wraps = []
+    if a.planned:
+        from . import BatchDecodeWrapper
+
+        for w in sets:
+            pw = BatchDecodeWrapper()
+            sh = w.shape
+            pw.plan_block_table(w.block_table, w.seq_lens, sh["num_q_heads"], sh["num_kv_heads"], sh["head_dim"],
+                                sh["page_size"], num_splits=a.num_splits or None)
+            wraps.append(pw)
     torch.cuda.synchronize()
     for i in range(a.calls):
         w = sets[i % n_sets]
-        paged_attention_decode_ex(*w.args(), num_splits=a.num_splits or None, engine=a.engine)
+        if a.planned:
+            wraps[i % n_sets].run(w.q, (w.k_cache, w.v_cache))
+        else:
+            paged_attention_decode_ex(*w.args(), num_splits=a.num_splits or None, engine=a.engine)
     torch.cuda.synchronize()
     used = [sets[i % n_sets] for i in range(a.calls)]
     mean_bytes = sum(wl.bytes_of(w) for w in used) / len(used)

@@ -73,14 +73,15 @@ def trace_row(root, name, ragged=False):
 
 
 def trace_table(rows):
-    hdr = (f"{'config':8s} {'calls':>5s} {'mean_us':>8s} {'median_us':>9s} {'min_us':>7s} {'max_us':>8s} "
+    w = max([8] + [len(r["config"]) for r in rows])
+    hdr = (f"{'config':{w}s} {'calls':>5s} {'mean_us':>8s} {'median_us':>9s} {'min_us':>7s} {'max_us':>8s} "
            f"{'alg_bytes':>12s} {'GB/s':>6s} {'%peak':>6s}  {'grid(x,y,z)':13s} {'wg':>4s} {'vgpr':>5s} {'lds':>4s} "
            f"{'sets':>4s}  template")
     out = [hdr]
     for r in rows:
         g = "({},{},{})".format(*r["grid"])
         t = re.search(r"<([^>]*)>", r["kernel"])
-        out.append(f"{r['config']:8s} {r['calls']:5d} {r['mean_us']:8.2f} {r['median_us']:9.2f} {r['min_us']:7.2f} "
+        out.append(f"{r['config']:{w}s} {r['calls']:5d} {r['mean_us']:8.2f} {r['median_us']:9.2f} {r['min_us']:7.2f} "
                    f"{r['max_us']:8.2f} {r['alg_bytes']:12d} {r['gbs']:6.0f} {r['pct_peak']:6.1f}  {g:13s} "
                    f"{r['wg']:4d} {r['vgpr']:>5s} {r['lds']:>4s} {r['sets']:4d}  <{t.group(1) if t else '?'}>")
     return "\n".join(out)
