@@ -9,6 +9,9 @@
 // stream of q's device, with
 // persistent split scratch (workspace + arrival counters) per (device,
 // stream).
+// plan_worklist / plan_worklist_csr and forward_worklist / forward_worklist_csr
+// split a decode into a plan (once per decode step) and runs (once per
+// layer) over pad_decode_plan_worklist / pad_decode_launch_worklist.
 // Argument errors surface as RuntimeError (the reference used TORCH_CHECK,
 // cuda/kernel_v4_split_k.cu:216-223).  No host synchronisation.
 
