@@ -948,38 +948,46 @@ struct SeqTable {
   int row[NK];    // CSR: offset of the sequence's page ids in `indices`
 };
 
-// All loads are issued before any is used (one memory round trip); a lane
-// past the batch re-reads the last sequence's entries and discards them, so
-// no branch separates the loads.
-template <int NK>
-__device__ __forceinline__ SeqTable<NK> load_seq_table(const Phase1Args& a, int lane) {
-  SeqTable<NK> t;
-  int r0[NK], r1[NK], r2[NK];
-  if (a.csr) {
+// Raw words of the sequence table for up to 256 sequences (lane l holds
+// sequences l + 64k): CSR indptr[b], indptr[b + 1] and last_page_len[b];
+// the dense table reads seq_lens[b] into all three.  A workgroup issues
+// these loads before its first page-id read and uses them after it, so the
+// two share one memory round trip; every load is unconditional (a lane past
+// the batch re-reads the last sequence's words), so no branch has to wait
+// for any of them.
+struct SeqRaw {
+  int r0[4], r1[4], r2[4];
+};
+
+__device__ __forceinline__ SeqRaw issue_seq_table(const Phase1Args& a, int lane) {
+  SeqRaw r;
+  const int32_t* p0 = a.csr ? a.indptr : a.sl;
+  const int32_t* p1 = a.csr ? a.indptr + 1 : a.sl;
+  const int32_t* p2 = a.csr ? a.lpl : a.sl;
+  const int64_t stride = a.csr ? 1 : a.ssl;
 #pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      const int b = min(lane + 64 * k, a.batch - 1);
-      r0[k] = a.indptr[b];
-      r1[k] = a.indptr[b + 1];
-      r2[k] = a.lpl[b];
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      r0[k] = a.sl[(int64_t)min(lane + 64 * k, a.batch - 1) * a.ssl];
-      r1[k] = r2[k] = 0;
-    }
+  for (int k = 0; k < 4; ++k) {
+    const int64_t off = (int64_t)min(lane + 64 * k, a.batch - 1) * stride;
+    r.r0[k] = p0[off];
+    r.r1[k] = p1[off];
+    r.r2[k] = p2[off];
   }
+  return r;
+}
+
+template <int NK>
+__device__ __forceinline__ SeqTable<NK> seq_table(const Phase1Args& a, const SeqRaw& r, int lane) {
+  SeqTable<NK> t;
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
     const bool in = lane + 64 * k < a.batch;
     int len, pages, row = 0;
     if (a.csr) {
-      row = min(max(r0[k], 0), a.max_pages);
-      pages = min(max(r1[k], row), a.max_pages) - row;
-      len = pages > 0 ? (pages - 1) * a.ps + min(max(r2[k], 1), a.ps) : 0;
+      row = min(max(r.r0[k], 0), a.max_pages);
+      pages = min(max(r.r1[k], row), a.max_pages) - row;
+      len = pages > 0 ? (pages - 1) * a.ps + min(max(r.r2[k], 1), a.ps) : 0;
     } else {
-      len = max(r0[k], 0);
+      len = max(r.r0[k], 0);
       pages = min(pages_for(a, len), a.max_pages);
     }
     t.len[k] = in ? len : 0;
@@ -1139,9 +1147,9 @@ __device__ __forceinline__ WorkItem static_item(const Phase1Args& a, int s, int 
 // units as CUs), each unit is one item of workgroup g = unit and the other
 // workgroups exit; otherwise plan the items.
 template <int NK>
-__device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int h, int bz, int g, int G, int lin,
-                                                 const int32_t* static_row, int lane) {
-  const SeqTable<NK> t = load_seq_table<NK>(a, lane);
+__device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, const SeqRaw& raw, int s, int h, int bz, int g,
+                                                 int G, int lin, const int32_t* static_row, int lane) {
+  const SeqTable<NK> t = seq_table<NK>(a, raw, lane);
   bool full = !a.csr;
 #pragma unroll
   for (int k = 0; k < NK; ++k)
@@ -1174,16 +1182,16 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, int s, int
 }
 
 // The work item of workgroup (s, h, bz) = slot g: the in-kernel plan when
-// a.balance is set, else the static split.  static_len is seq_lens[bz]
-// (dense) or any word (CSR).  The decode kernel and the work-list planner
-// both call this, so a planned launch runs exactly the items of an
-// unplanned one.
-__device__ __forceinline__ WorkItem resolve_workgroup(const Phase1Args& a, int s, int h, int bz, int g, int G,
-                                                      int lin, const int32_t* static_row, int static_len,
-                                                      int lane) {
+// a.balance is set, else the static split.  raw is issue_seq_table()'s
+// loads; static_len is seq_lens[bz] (dense) or any word (CSR).  The decode
+// kernel and the work-list planner both call this, so a planned launch runs
+// exactly the items of an unplanned one.
+__device__ __forceinline__ WorkItem resolve_workgroup(const Phase1Args& a, const SeqRaw& raw, int s, int h, int bz,
+                                                      int g, int G, int lin, const int32_t* static_row,
+                                                      int static_len, int lane) {
   if (a.balance) {
-    if (a.batch <= 64) return resolve_item<1>(a, s, h, bz, g, G, lin, static_row, lane);
-    return resolve_item<4>(a, s, h, bz, g, G, lin, static_row, lane);
+    if (a.batch <= 64) return resolve_item<1>(a, raw, s, h, bz, g, G, lin, static_row, lane);
+    return resolve_item<4>(a, raw, s, h, bz, g, G, lin, static_row, lane);
   }
   if (a.csr) {
     int row, pages, L;
@@ -1217,6 +1225,12 @@ __device__ __forceinline__ bool worklist_item(const Phase1Args& a, int g, int G,
 #pragma unroll
   for (int i = 0; i < 10; ++i) f[i] = load_uniform_i32(r + i);
   pid = load_uniform_i32(r + 16 + wave);
+  // The record's values are only used past the header check, so the
+  // compiler would sink their loads below it: a second round trip.  Pinning
+  // them here keeps the header and the record in one.
+#pragma unroll
+  for (int i = 0; i < 10; ++i) asm volatile("" : "+s"(f[i]));
+  asm volatile("" : "+s"(pid));
   if (magic != kWlMagic || key != a.wl_key) return false;
   w.b = f[0];
   w.kvh = f[1];
@@ -1287,8 +1301,9 @@ __global__ __launch_bounds__(64) void pad_plan_kernel(const Phase1Args a, int32_
   const int g = s + a.num_splits * (h + a.hkv * bz);
   const int G = a.num_splits * a.hkv * a.batch;
   const int32_t* static_row = a.bt + (int64_t)bz * a.sbb;
+  const SeqRaw raw = issue_seq_table(a, lane);
   const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)bz * a.ssl);
-  const WorkItem it = resolve_workgroup(a, s, h, bz, g, G, lin, static_row, static_len, lane);
+  const WorkItem it = resolve_workgroup(a, raw, s, h, bz, g, G, lin, static_row, static_len, lane);
   int v = 0;
   switch (lane) {
     case 0: v = it.b; break;
@@ -1355,14 +1370,20 @@ void pad_phase1_kernel(const Phase1Args a) {
   if (a.worklist != nullptr && worklist_item(a, g, G, wave, it, phys_first)) {
     first_known = true;
   } else {
+    // The sequence table's loads go first, then the page id and this
+    // workgroup's sequence length: one round trip for all of them.  The
+    // page-id read has no branch (a CSR index or an empty table reads a
+    // valid word that is never used), as a value loaded under a branch
+    // would be waited for where the branch joins, before the later loads.
+    const SeqRaw raw = issue_seq_table(a, lane);
     const int32_t* static_row = a.bt + (int64_t)bz * a.sbb;
     if constexpr (ENGINE == 0 && MODE == kModeUniform) {
-      if (!a.csr) phys_first = first_page_id(a, static_row, a.sbp, a.max_pages - 1, s * a.pps, wave);
+      const int col = min(s * a.pps + block_page(a, wave), a.max_pages - 1);
+      const bool use = !a.csr && a.max_pages > 0;
+      phys_first = load_uniform_i32(use ? static_row + (int64_t)col * a.sbp : (a.csr ? a.indptr : a.sl));
     }
-    // Read unconditionally (any valid word when unused) after the page id, so
-    // both reads share one round trip.
     const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)bz * a.ssl);
-    it = resolve_workgroup(a, s, h, bz, g, G, lin, static_row, static_len, lane);
+    it = resolve_workgroup(a, raw, s, h, bz, g, G, lin, static_row, static_len, lane);
     first_known = !a.csr && it.b == bz && it.p_begin == s * a.pps;
   }
   PAD_TL(lin, PAD_TL_ITEM);
