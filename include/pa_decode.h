@@ -15,7 +15,7 @@
  *   q           fp16 [batch, num_q_heads, head_dim]
  *   k_cache     fp16 [num_pages, page_size, num_kv_heads, head_dim]
  *   v_cache     fp16 [num_pages, page_size, num_kv_heads, head_dim]
- *   block_table int32 [batch, max_pages]
+ *   block_table int32 [batch, max_pages] (may be NULL when max_pages is 0)
  *   seq_lens    int32 [batch]
  *   out         fp16 [batch, num_q_heads, head_dim]
  * head_dim must be contiguous (stride 1) for q, k_cache, v_cache and out.

@@ -1854,7 +1854,9 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   if (engine == 1 && !valu_supported(d->head_dim, gqa)) return PAD_ERR_UNSUPPORTED_GQA;
   L->empty = d->batch == 0;
   if (L->empty) return PAD_OK;
-  if (csr ? (!indptr || !lpl || (!bt && d->max_pages > 0)) : (!bt || !sl)) return PAD_ERR_NULL_POINTER;
+  // The page-id array may be NULL only when it has no entries (a [batch, 0]
+  // table, or an empty CSR index): then no sequence has a page to read.
+  if ((!bt && d->max_pages > 0) || (csr ? (!indptr || !lpl) : !sl)) return PAD_ERR_NULL_POINTER;
   if (io) {
     if (!q || !k || !v || !out) return PAD_ERR_NULL_POINTER;
     // 16-byte rows: every K/V/q/out row start must be 16-byte aligned.

@@ -360,3 +360,17 @@ def test_csr_fuzz_wide(seed):
     ps = k.shape[1]
     for s in (None, 7, 100):
         _check_csr(q, k, v, bt, sl, ps, num_splits=s)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("num_splits", [None, 1, 4])
+def test_csr_index_without_pages_gives_zeros(num_splits):
+    # Every sequence empty: indptr all zero and no entries in indices (its
+    # data pointer may be NULL); the oracle gives zeros.
+    k, v = make_cache(2, 16, 2, 128, seed=7)
+    q = torch.randn(3, 12, 128, generator=torch.Generator().manual_seed(7))
+    indptr = torch.zeros(4, dtype=torch.int32)
+    indices = torch.zeros(0, dtype=torch.int32)
+    last = torch.full((3,), 16, dtype=torch.int32)
+    out = _run_csr(q, k, v, indptr, indices, last, num_splits=num_splits)
+    assert out.shape == q.shape and torch.all(out == 0)

@@ -197,6 +197,19 @@ def test_zero_length_rows_give_zeros(engine):
 
 
 @pytest.mark.parametrize("engine", ENGINES)
+def test_block_table_without_columns_gives_zeros(engine):
+    # A [batch, 0] table (every sequence empty) is valid input: the oracle
+    # returns zeros, and the kernel must not read a page id for it.
+    k, v = make_cache(2, 16, 2, 128, seed=6)
+    q = torch.randn(3, 8, 128, generator=torch.Generator().manual_seed(6))
+    bt = torch.zeros(3, 0, dtype=torch.int32)
+    sl = torch.zeros(3, dtype=torch.int32)
+    for s in (None, 1, 4):
+        out = _check(q, k, v, bt, sl, engine, s)
+        assert torch.all(out == 0)
+
+
+@pytest.mark.parametrize("engine", ENGINES)
 def test_poisoned_holes_and_nan_slots(engine):
     # Unused columns/pages and the unused tail slots of the last page hold
     # NaN: a kernel that reads or weights any of them produces NaN.
