@@ -76,6 +76,8 @@ def _lens(kind, seed):
         lens = [rng.randint(0, 900) for _ in range(12)]
         lens[3] = lens[7] = 0
         return lens, 16
+    if kind == "allempty":  # no sequence has a page (the CSR index has no entries)
+        return [0] * 5, 16
     raise ValueError(kind)
 
 
@@ -90,6 +92,7 @@ GPU_CASES = [
     ("empty", 2, 6, 128, 16, None),
     ("empty", 2, 6, 64, 8, None),  # sub-page blocks
     ("empty", 1, 8, 128, 12, None),  # generic page size
+    ("allempty", 2, 6, 128, 16, None),
     ("ragged100", 4, 4, 256, 16, None),
 ]
 
@@ -117,7 +120,7 @@ def test_planned_run_equals_in_kernel_plan(kind, hkv, group, d, ps, num_splits):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind", ["ragged32", "empty", "oversub"])
+@pytest.mark.parametrize("kind", ["ragged32", "empty", "oversub", "allempty"])
 def test_planned_csr_run_equals_in_kernel_plan(kind):
     import paged_attention_decode_amd as pad
 
