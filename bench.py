@@ -53,6 +53,10 @@ What one run measures (one GPU; ``--gpus`` above 1 exits with a message):
   all layers), cold throughput.
 * ``c2_sweep[b].us_per_call_cold_planned``: the same plan-once-run-many
   timing for each batch of C2.
+* ``cpu_baseline_configs`` (only with ``--cpu-configs``): the CPU oracle
+  next to the GPU call on each listed configuration, with the sample sizes
+  the reference's bench conventions suggest (median of 5 calls on C1-C3, one
+  call on C4, 8 seeded rows of C5); a table of it goes to stderr.
 """
 
 from __future__ import annotations
@@ -92,6 +96,9 @@ def _parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--cpu-threads", type=int, default=16,
                    help="most CPU threads for the baseline (a GPU box grants one GPU 16 cores)")
+    p.add_argument("--cpu-configs", default="",
+                   help="also time the CPU oracle on these configurations (e.g. C1,C2:16,C2:64,C3,C4,C5) "
+                        "next to the GPU call; adds cpu_baseline_configs to the JSON line and a table on stderr")
     p.add_argument("--trials", type=int, default=15)
     p.add_argument("--sweep-calls", type=int, default=200, help="cold back-to-back calls per C2 sweep batch")
     return p.parse_args()
@@ -298,6 +305,97 @@ def _cpu_baseline(w, seconds, gpu_out, max_threads):
     return statistics.median(times), len(times), torch.get_num_threads(), err
 
 
+def _cpu_inputs(w, rows):
+    """Host fp32 inputs of batch `rows` of w: only the pages those rows use, relabelled."""
+    import torch
+
+    ps = w.k_cache.shape[1]
+    bt = w.block_table[rows].cpu().to(torch.long)
+    sl = w.seq_lens[rows].cpu().to(torch.long)
+    cols = [bt[i, :-(-int(sl[i]) // ps)] for i in range(len(rows))]
+    pages = torch.unique(torch.cat(cols)) if cols else torch.zeros(0, dtype=torch.long)
+    relabel = torch.full((int(pages.max()) + 1 if pages.numel() else 1,), -1, dtype=torch.long)
+    relabel[pages] = torch.arange(pages.numel())
+    bt_new = torch.zeros_like(bt)
+    for i, c in enumerate(cols):
+        bt_new[i, :c.numel()] = relabel[c]
+    idx = pages.to(w.k_cache.device)
+    k = w.k_cache.index_select(0, idx).float().cpu()
+    v = w.v_cache.index_select(0, idx).float().cpu()
+    return w.q[rows].float().cpu(), k, v, bt_new, sl
+
+
+def _cpu_configs(pad, wl, specs, engine, splits, max_threads, seconds=3.0):
+    """The fp32 CPU oracle next to the GPU call on several configurations.
+
+    Per configuration: GPU seconds per call over back-to-back cold calls
+    (inputs rotated as in the sweep; C5 is one 17 GB set); CPU seconds per
+    call of oracle/reference.py on the host cores after one untimed call:
+    the median over at least 5 calls (C1-C3) or 1 call (C4, and C5 over 8
+    seeded rows, their pages only), repeated for about `seconds` per
+    configuration (at most 50 calls), compared per algorithmic byte.  Every GPU timing runs before the first
+    CPU call, so the oracle's worker threads never compete with the launch
+    thread.  Returns (records, table text)."""
+    import random
+
+    import torch
+
+    from oracle.reference import paged_attention_decode_reference
+
+    staged = []
+    for spec in specs:
+        name, _, b = spec.partition(":")
+        batch = int(b) if b else None
+        w = wl.make(name, batch=batch, seed=3000)
+        n_sets = 1 if name == "C5" else _rotation(w.k_cache.numel() * 4)
+        sets = [w] + [wl.make(name, batch=batch, seed=3000 + i) for i in range(1, n_sets)]
+        calls = 10 if name == "C5" else 200
+        # The first pass brings the clocks up after the inputs were made; the second is kept.
+        _throughput(pad, sets, engine, splits, calls, 5 if name == "C5" else 20)
+        gpu_s = _throughput(pad, sets, engine, splits, calls, 5 if name == "C5" else 20)
+        del sets[1:]
+        if name == "C5":
+            rows = sorted(random.Random(3000).sample(range(w.batch), 8))
+            runs, sample = 1, "8 seeded rows, their pages only"
+        else:
+            rows = list(range(w.batch))
+            runs, sample = (1, "whole batch") if name == "C4" else (5, "whole batch")
+        gpu_rows = _call(pad, w, engine, splits)[rows].float().cpu()
+        staged.append((spec, w.scale, wl.bytes_of(w), dict(w.shape), w.k_cache.shape[1], gpu_s, gpu_rows, runs,
+                       sample, _cpu_inputs(w, rows)))
+        del w
+        torch.cuda.empty_cache()
+    cores = max(1, min(len(os.sched_getaffinity(0)), max_threads))
+    torch.set_num_threads(cores)
+    recs = []
+    for spec, scale, nb_gpu, shape, ps, gpu_s, gpu_rows, runs, sample, (q, k, v, bt, sl) in staged:
+        paged_attention_decode_reference(q, k, v, bt, sl, scale)  # untimed: first-touch of its buffers
+        times, out = [], None
+        t_start = time.perf_counter()
+        while len(times) < runs or (time.perf_counter() - t_start < seconds and len(times) < 50):
+            t0 = time.perf_counter()
+            out = paged_attention_decode_reference(q, k, v, bt, sl, scale)
+            times.append(time.perf_counter() - t0)
+        cpu_s = statistics.median(times)
+        hkv, hq, d = shape["num_kv_heads"], shape["num_q_heads"], shape["head_dim"]
+        lens = sl.tolist()
+        nb_cpu = (sum(lens) * hkv * d * 4 + 4 * len(lens) * hq * d + sum(-(-n // ps) for n in lens) * 4
+                  + 4 * len(lens))
+        recs.append({"config": spec, "gpu_us_per_call": round(gpu_s * 1e6, 2),
+                     "gpu_gbs": round(nb_gpu / gpu_s / 1e9, 1), "cpu_ms_per_call": round(cpu_s * 1e3, 2),
+                     "cpu_gbs": round(nb_cpu / cpu_s / 1e9, 3), "cpu_calls": len(times), "cpu_sample": sample,
+                     "cpu_threads": torch.get_num_threads(),
+                     "gpu_over_cpu": round(nb_gpu / gpu_s / (nb_cpu / cpu_s), 1),
+                     "max_abs_err": float((gpu_rows - out).abs().max())})
+    lines = [f"{'config':8s} {'GPU us/call':>12s} {'GPU GB/s':>9s} {'CPU ms/call':>12s} {'CPU GB/s':>9s} "
+             f"{'GPU/CPU':>8s} {'max|err|':>9s}  CPU sample (calls, threads)"]
+    for r in recs:
+        lines.append(f"{r['config']:8s} {r['gpu_us_per_call']:12.2f} {r['gpu_gbs']:9.1f} {r['cpu_ms_per_call']:12.2f} "
+                     f"{r['cpu_gbs']:9.3f} {r['gpu_over_cpu']:8.1f} {r['max_abs_err']:9.1e}  {r['cpu_sample']} "
+                     f"({r['cpu_calls']}, {r['cpu_threads']})")
+    return recs, "\n".join(lines)
+
+
 def main():
     args = _parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -445,6 +543,12 @@ def main():
             del rs, w
         result["c2_sweep"] = sweep
 
+    # Before the headline's CPU baseline: its timings are all GPU ones first.
+    if args.cpu_configs:
+        recs, table = _cpu_configs(pad, wl, [s for s in args.cpu_configs.split(",") if s], engine, splits,
+                                   args.cpu_threads)
+        result["cpu_baseline_configs"] = recs
+        print(table, file=sys.stderr, flush=True)
     if not args.no_cpu:
         gpu_out = _call(pad, probe, engine, splits)
         torch.cuda.synchronize()
