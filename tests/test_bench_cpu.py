@@ -1,0 +1,53 @@
+"""CPU checks of bench.py's host-side logic (no GPU).
+
+``_cpu_inputs`` copies only the pages a subset of batch rows uses and
+relabels their block-table columns onto that compact page set, so the CPU
+baseline on C5 never upcasts the whole 17 GB cache.  The relabelled inputs
+must decode exactly as the full ones do for those rows.
+"""
+
+from __future__ import annotations
+
+import importlib.util
+import os
+
+import torch
+
+from oracle.reference import paged_attention_decode_reference
+from paged_attention_decode_amd import workloads as wl
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _bench():
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(REPO, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_row_subset_inputs_decode_like_the_full_batch():
+    bench = _bench()
+    w = wl.make("C3", seed=7, device="cpu")  # ragged lengths, page 32, shuffled table
+    rows = [0, 5, 17, 31]
+    q, k, v, bt, sl = bench._cpu_inputs(w, rows)
+    used = sum(-(-int(w.seq_lens[r]) // w.k_cache.shape[1]) for r in rows)
+    assert k.shape[0] == len(torch.unique(torch.cat(
+        [w.block_table[r, :-(-int(w.seq_lens[r]) // w.k_cache.shape[1])] for r in rows]))) <= used
+    assert torch.equal(sl, w.seq_lens[rows].to(torch.long))
+    sub = paged_attention_decode_reference(q, k, v, bt, sl, w.scale)
+    full = paged_attention_decode_reference(w.q.float(), w.k_cache.float(), w.v_cache.float(), w.block_table,
+                                            w.seq_lens, w.scale)
+    torch.testing.assert_close(sub, full[rows], rtol=0, atol=0)
+
+
+def test_row_subset_with_an_empty_row():
+    bench = _bench()
+    w = wl.make("C2", batch=3, seed=8, device="cpu")
+    w.seq_lens[1] = 0
+    q, k, v, bt, sl = bench._cpu_inputs(w, [0, 1])
+    out = paged_attention_decode_reference(q, k, v, bt, sl, w.scale)
+    assert torch.all(out[1] == 0)
+    full = paged_attention_decode_reference(w.q.float(), w.k_cache.float(), w.v_cache.float(), w.block_table,
+                                            w.seq_lens, w.scale)
+    torch.testing.assert_close(out[0], full[0], rtol=0, atol=0)
