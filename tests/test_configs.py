@@ -5,7 +5,9 @@ C1-C4 are checked whole against the fp32 oracle on the same fp16 inputs
 ~17 GB of K/V) is checked on a seeded subset of 8 rows (the oracle gathers
 only their pages), and on size-independent properties over the whole batch:
 every output finite and inside the convex hull bound |out| <= max |V|, rows
-equal to the same rows decoded alone, and bit-identical repeats.
+equal to the same rows decoded alone, and bit-identical repeats.  C3 and C5
+planned once (BatchDecodeWrapper, dense and CSR) give bit-identical outputs
+to the in-kernel plan at full size.
 """
 
 from __future__ import annotations
@@ -70,3 +72,24 @@ def test_c5_serving_batch_subset_and_properties():
     torch.testing.assert_close(solo.float(), out[rows].float(), rtol=2e-3, atol=1e-3)
     # int64 offsets: the cache spans more than 2^31 elements.
     assert w.k_cache.numel() > 2**31
+
+
+@pytest.mark.parametrize("name", ["C3", "C5"])
+def test_ragged_configs_planned_once_match_in_kernel_plan(name):
+    # Plan once / run many (BatchDecodeWrapper) at full size: the work list
+    # holds the in-kernel planner's items, so every row is bit-identical,
+    # over the dense table and over the CSR index of the same batch.
+    import paged_attention_decode_amd as pad
+    from paged_attention_decode_amd import workloads as wl
+
+    w = wl.make(name, seed=6)
+    q, k, v, bt, sl = w.args()
+    sh = w.shape
+    dense = pad.BatchDecodeWrapper()
+    dense.plan_block_table(bt, sl, sh["num_q_heads"], sh["num_kv_heads"], sh["head_dim"], sh["page_size"])
+    assert torch.equal(dense.run(q, (k, v)), _decode(w))
+    indptr, indices, last = pad.paged_kv_indices(bt, sl, sh["page_size"])
+    csr = pad.BatchDecodeWrapper()
+    csr.plan(indptr, indices, last, sh["num_q_heads"], sh["num_kv_heads"], sh["head_dim"], sh["page_size"])
+    assert torch.equal(csr.run(q, (k, v)), pad.paged_attention_decode_csr(q, k, v, indptr, indices, last))
+    torch.cuda.synchronize()
