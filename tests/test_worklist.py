@@ -13,7 +13,13 @@ FlashInfer-style ``plan(indptr, indices, last_page_len, ...)`` /
 ``run(q, (k_cache, v_cache))`` surface is checked against the fp32 oracle
 on the cases of the reference's tests/test_flashinfer_adapter.py:34-136.
 
-CPU: the work-list size is a header plus one record per workgroup.
+The lists themselves are checked for structure: every (sequence, kv head)
+unit's pages are covered by its items exactly once and in order, an empty
+unit has the one item that writes its zero rows, the item slots of a unit
+are its own contiguous range, and each wave's first page id is the table's.
+
+CPU: the work-list size is a header plus one record per workgroup; the
+structure check rejects planted mistakes in a hand-built list.
 """
 
 from __future__ import annotations
@@ -240,3 +246,120 @@ def test_list_from_other_lengths_keeps_scratch_consistent():
     assert_parity(out, decode_fp16_protocol(q.float(), k.float(), v.float(), bt, torch.tensor(lens_b)))
     out_a = w.run(qc, (kc, vc))
     assert torch.equal(out_a, pad.paged_attention_decode(qc, kc, vc, btc, sla))
+
+
+# ---------------------------------------------------------------- plan structure
+WL_INTS = WL_RECORD_BYTES // 4
+
+
+def _check_plan_structure(wl, lens, ps, hkv, bt_rows, nw, max_pages):
+    """The items a work list holds cover every (sequence, kv head) unit's pages exactly once.
+
+    wl: the list as int32 on the host; lens: sequence lengths; bt_rows[b]: the
+    page ids of sequence b in order (its row of the dense table, or its CSR
+    slice); nw: waves per workgroup."""
+    assert wl[0] == 0x574C4150
+    G = int(wl[2])
+    recs = wl[WL_INTS:WL_INTS + WL_INTS * G].view(G, WL_INTS)
+    units = {}
+    for g in range(G):
+        r = recs[g].tolist()
+        b, kvh, p0, p1, L, nsplit, slot0, col_max, valid = r[:9]
+        if not valid:
+            continue
+        assert 0 <= b < len(lens) and 0 <= kvh < hkv and L == lens[b]
+        pages = min(-(-L // ps), max_pages)
+        units.setdefault((b, kvh), []).append((p0, p1, g, nsplit, slot0))
+        if pages == 0:
+            assert nsplit == 0
+            continue
+        assert 0 <= p0 < p1 <= pages and slot0 <= g < slot0 + nsplit and col_max >= p1 - 1
+        if ps % 16 == 0:  # whole-page blocks: each wave's first page id is in the record
+            for w in range(nw):
+                col = min(p0 + (w * 16) // ps, col_max)
+                assert r[16 + w] == int(bt_rows[b][col]), (g, w)
+    slots = []
+    for b, L in enumerate(lens):
+        pages = min(-(-L // ps), max_pages)
+        for kvh in range(hkv):
+            items = sorted(units.get((b, kvh), []))
+            if pages == 0:
+                assert len(items) == 1, (b, kvh)  # one workgroup writes the zero rows
+                continue
+            assert len(items) == items[0][3], (b, kvh)  # nsplit items
+            assert items[0][0] == 0 and items[-1][1] == pages, (b, kvh)
+            for (_, e, *_), (s, *_) in zip(items, items[1:]):
+                assert e == s, (b, kvh)  # contiguous, no overlap
+            slot0 = items[0][4]
+            assert all(it[4] == slot0 for it in items)
+            assert sorted(it[2] for it in items) == list(range(slot0, slot0 + len(items)))
+            slots.append((slot0, slot0 + len(items)))
+    slots.sort()
+    for (_, e), (s, _) in zip(slots, slots[1:]):
+        assert e <= s  # units' slot ranges are disjoint
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind,ps,csr", [("ragged32", 32, False), ("ragged100", 16, False), ("oversub", 16, False),
+                                         ("full16", 16, False), ("empty", 16, False), ("allempty", 16, False),
+                                         ("ragged32", 32, True), ("empty", 8, True)])
+def test_work_list_covers_every_page_once(kind, ps, csr):
+    import paged_attention_decode_amd as pad
+    from paged_attention_decode_amd._native import ext
+
+    lens, seed = _lens(kind, 31)
+    hkv, group = 2, 6
+    q, k, v, bt, sl = _dense_case(lens, hkv, group, 128, ps, seed)
+    if csr:
+        indptr, indices, last = pad.paged_kv_indices(bt, sl, ps)
+        wl = ext().plan_worklist_csr(indptr, indices, last, hkv * group, hkv, 128, ps, 0)
+        ip = indptr.cpu().tolist()
+        rows = [indices.cpu()[ip[b]:ip[b + 1]].tolist() for b in range(len(lens))]
+        max_pages = 1 << 30
+        nw = pad.plan(len(lens), hkv * group, hkv, 128, ps, max(indices.numel(), 1), csr=True)["waves_per_group"]
+    else:
+        wl = ext().plan_worklist(bt, sl, hkv * group, hkv, 128, ps, 0)
+        rows = bt.cpu().tolist()
+        max_pages = bt.shape[1]
+        nw = pad.plan(len(lens), hkv * group, hkv, 128, ps, max_pages)["waves_per_group"]
+    torch.cuda.synchronize()
+    _check_plan_structure(wl.cpu().view(torch.int32), lens, ps, hkv, rows, nw, max_pages)
+
+
+def _synthetic_list():
+    # Two sequences of 5 and 0 pages (page size 16), one kv head, 4 slots:
+    # sequence 0 in items [0, 3) and [3, 5) (slots 0, 1), sequence 1's zero
+    # rows in slot 2, slot 3 without an item.
+    wl = torch.zeros(WL_INTS * 5, dtype=torch.int32)
+    wl[0], wl[2] = 0x574C4150, 4
+    rows = [[10, 11, 12, 13, 14, 15], [20, 21, 22, 23, 24, 25]]
+
+    def rec(g, vals, pids):
+        base = WL_INTS * (1 + g)
+        wl[base:base + len(vals)] = torch.tensor(vals, dtype=torch.int32)
+        wl[base + 16:base + 16 + len(pids)] = torch.tensor(pids, dtype=torch.int32)
+
+    # b, kvh, p_begin, p_end, L, nsplit, slot0, col_max, valid, row
+    rec(0, [0, 0, 0, 3, 70, 2, 0, 5, 1, 0], [10, 11])
+    rec(1, [0, 0, 3, 5, 70, 2, 0, 5, 1, 0], [13, 14])
+    rec(2, [1, 0, 0, 0, 0, 0, 2, -1, 1, 0], [])
+    return wl, rows
+
+
+def test_plan_structure_check_catches_planted_mistakes():
+    lens, ps, hkv, nw, max_pages = [70, 0], 16, 1, 2, 6
+    wl, rows = _synthetic_list()
+    _check_plan_structure(wl, lens, ps, hkv, rows, nw, max_pages)
+    base = WL_INTS
+    mistakes = [
+        (base * 2 + 2, 2),   # second item starts inside the first: overlap
+        (base * 2 + 3, 4),   # a page left uncovered at the end
+        (base * 1 + 16, 12),  # wrong first page id of wave 0
+        (base * 2 + 6, 1),   # inconsistent slot0 inside a unit
+        (base * 3 + 8, 0),   # the empty sequence's zero rows have no item
+    ]
+    for idx, val in mistakes:
+        bad = wl.clone()
+        bad[idx] = val
+        with pytest.raises(AssertionError):
+            _check_plan_structure(bad, lens, ps, hkv, rows, nw, max_pages)
