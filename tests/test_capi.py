@@ -102,6 +102,33 @@ def test_plan_matches_python_mirror(batch, hq, hkv, d, ps, max_pages, splits, cu
     assert nc.value == m.counters
 
 
+def test_plan_mirror_on_random_shapes():
+    # 600 seeded shapes across every regime the heuristic has (latency-bound,
+    # bandwidth-bound, oversubscribed, explicit splits, narrow rows, head_dim
+    # 256, odd page sizes, CU counts other than 256), dense and CSR.
+    import random
+
+    lib = _native.capi()
+    rng = random.Random(2024)
+    for _ in range(600):
+        hkv = rng.choice([1, 2, 4, 8])
+        hq = hkv * rng.choice([1, 2, 4, 6, 8, 16])
+        d = rng.choice([32, 64, 96, 128, 256])
+        ps = rng.choice([1, 2, 3, 8, 12, 16, 24, 32, 64])
+        batch = rng.choice([1, 2, 3, 8, 16, 33, 64, 100, 256, 300])
+        max_pages = rng.choice([1, 5, 64, 256, 1000, 8192])
+        splits = rng.choice([0, 0, 0, 1, 4, 64])
+        cus = rng.choice([256, 256, 80, 0])
+        csr = rng.random() < 0.3
+        p = _native.PadPlan()
+        fn = lib.pad_decode_plan_csr if csr else lib.pad_decode_plan
+        assert fn(ctypes.byref(_dims(batch, hq, hkv, d, ps, max_pages)), splits, cus, ctypes.byref(p)) == 0
+        m = heuristics.plan(batch, hq, hkv, d, ps, max_pages, splits, cus, csr=csr)
+        got = (p.num_splits, p.pages_per_split, p.waves_per_group, bool(p.single_pass), p.workspace_bytes, p.counters)
+        assert got == (m.num_splits, m.pages_per_split, m.waves_per_group, m.single_pass, m.workspace_bytes,
+                       m.counters), (batch, hq, hkv, d, ps, max_pages, splits, cus, csr)
+
+
 @pytest.mark.parametrize("batch,hq,hkv,d,ps,nnz,splits", [
     (1, 12, 2, 128, 16, 256, 0),
     (16, 12, 2, 128, 16, 16 * 256, 0),
