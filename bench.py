@@ -21,12 +21,17 @@ What one run measures (one GPU; ``--gpus`` above 1 exits with a message):
   committed in profiles/traffic.json (``traffic_source`` names the file and
   the commit that last changed it); ``fetch_gbs`` = traffic / us_per_call,
   north_star's "FETCH_SIZE / kernel time" with the same conservative time.
-  ``kernel_trace_us`` is the mean kernel duration rocprofv3 measured for
-  the same configuration (profiles/pad_phase1_kernel_configs_kernel_trace.txt).
+  ``kernel_trace_us_committed`` is the mean kernel duration rocprofv3
+  measured for the same configuration in another run, read from the
+  committed profiles/pad_phase1_kernel_configs_kernel_trace.txt
+  (``kernel_trace_source`` names the file and the kernel's commit);
+  ``timed_region_wall_s`` is the host wall clock of the K timed calls alone
+  (synchronize to synchronize, warm-up excluded).
 * ``c2_sweep``: for every batch of C2, the reference's latency method
   (bench/bench_decode.py:86-112 of the reference: each call bracketed by
   events and followed by a sync, best of 30 after 10 warm-up calls, median
-  of 15 trials, warm inputs) and the cold steady-state throughput of
+  of 15 trials, warm inputs; ``us_per_call_warm_trials`` holds the 15
+  per-trial values) and the cold steady-state throughput of
   ``--sweep-calls`` back-to-back calls (rotated KV caches), independent of
   ``--steps`` so that the first call's host-side latency is spread over
   enough calls.
@@ -53,10 +58,11 @@ What one run measures (one GPU; ``--gpus`` above 1 exits with a message):
   all layers), cold throughput.
 * ``c2_sweep[b].us_per_call_cold_planned``: the same plan-once-run-many
   timing for each batch of C2.
-* ``cpu_baseline_configs`` (only with ``--cpu-configs``): the CPU oracle
-  next to the GPU call on each listed configuration, with the sample sizes
-  the reference's bench conventions suggest (median of 5 calls on C1-C3, one
-  call on C4, 8 seeded rows of C5); a table of it goes to stderr.
+* ``cpu_baseline_configs`` (``--cpu-configs``, by default C1, C3, C4 and
+  C5; ``none`` skips it): the CPU oracle next to the GPU call on each listed
+  configuration in the same run, with the sample sizes the reference's bench
+  conventions suggest (median of at least 5 calls on C1-C3, one call on C4,
+  8 seeded rows of C5); a table of it goes to stderr.
 """
 
 from __future__ import annotations
@@ -65,6 +71,7 @@ import argparse
 import json
 import math
 import os
+import re
 import statistics
 import subprocess
 import sys
@@ -96,9 +103,10 @@ def _parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--cpu-threads", type=int, default=16,
                    help="most CPU threads for the baseline (a GPU box grants one GPU 16 cores)")
-    p.add_argument("--cpu-configs", default="",
+    p.add_argument("--cpu-configs", default="C1,C3,C4,C5",
                    help="also time the CPU oracle on these configurations (e.g. C1,C2:16,C2:64,C3,C4,C5) "
-                        "next to the GPU call; adds cpu_baseline_configs to the JSON line and a table on stderr")
+                        "next to the GPU call; adds cpu_baseline_configs to the JSON line and a table on "
+                        "stderr ('none' skips it)")
     p.add_argument("--trials", type=int, default=15)
     p.add_argument("--sweep-calls", type=int, default=200, help="cold back-to-back calls per C2 sweep batch")
     return p.parse_args()
@@ -116,19 +124,26 @@ def _call(pad, w, engine, splits):
     return pad.paged_attention_decode_ex(*w.args(), num_splits=splits or None, engine=engine)
 
 
-def _throughput(pad, sets, engine, splits, steps, warmup):
-    """Seconds per call over `steps` back-to-back calls (events on the launch stream)."""
+def _throughput(pad, sets, engine, splits, steps, warmup, wall=None):
+    """Seconds per call over `steps` back-to-back calls (events on the launch stream).
+
+    With a list `wall`, also appends the host wall-clock seconds of the timed
+    region alone: from the synchronize before the first timed call to the
+    synchronize after the last (the warm-up calls are outside it)."""
     import torch
 
     for i in range(warmup):
         _call(pad, sets[i % len(sets)], engine, splits)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
     start.record()
     for i in range(steps):
         _call(pad, sets[i % len(sets)], engine, splits)
     end.record()
     torch.cuda.synchronize()
+    if wall is not None:
+        wall.append(time.perf_counter() - t0)
     return start.elapsed_time(end) / 1e3 / steps
 
 
@@ -161,7 +176,9 @@ def _throughput_planned(pad, sets, splits, steps, warmup):
 
 
 def _latency_reference_method(pad, w, engine, splits, trials):
-    """bench/bench_decode.py:86-112 of the reference: median of best-of-30 event timings."""
+    """bench/bench_decode.py:86-112 of the reference: median of best-of-30 event timings.
+
+    Returns (median µs, the per-trial best-of-30 values in µs)."""
     import torch
 
     def once():
@@ -178,7 +195,8 @@ def _latency_reference_method(pad, w, engine, splits, trials):
             best = min(best, s.elapsed_time(e))
         return best
 
-    return statistics.median([once() for _ in range(trials)]) * 1e3  # µs
+    samples = [once() * 1e3 for _ in range(trials)]  # µs
+    return statistics.median(samples), samples
 
 
 def _git_last_commit(relpath):
@@ -212,18 +230,30 @@ def _traffic(workload_name):
 
 
 def _kernel_trace_us(workload_name):
-    """Mean kernel duration rocprofv3 recorded for this configuration in the committed kernel-trace summary."""
-    path = os.path.join(REPO, "profiles", "pad_phase1_kernel_configs_kernel_trace.txt")
+    """(mean µs, provenance) rocprofv3 recorded for this configuration in the committed kernel-trace summary.
+
+    The number comes from the committed profile (another run, on another
+    box), not from this run; the provenance names the file and the commit
+    its measurement was taken at (its "commit" line)."""
+    rel = os.path.join("profiles", "pad_phase1_kernel_configs_kernel_trace.txt")
+    path = os.path.join(REPO, rel)
     if not os.path.exists(path):
-        return None
+        return None, None
+    us, commit = None, None
     for line in open(path):
         f = line.split()
-        if len(f) > 3 and f[0] == workload_name:
+        m = re.search(r"kernel at commit ([0-9a-f]{7,40})", line)
+        if m and commit is None:
+            commit = m.group(1)
+        if us is None and len(f) > 3 and f[0] == workload_name:
             try:
-                return float(f[2])
+                us = float(f[2])
             except ValueError:
-                return None
-    return None
+                pass
+    if us is None:
+        return None, None
+    return us, (f"{rel} (a committed rocprofv3 --kernel-trace --stats summary of another run; kernel at commit "
+                f"{commit or _git_last_commit(rel) or 'unknown'})")
 
 
 def _run_json(cmd, timeout=30):
@@ -425,10 +455,10 @@ def main():
                     shp["max_pages"], splits)
 
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    sec = _throughput(pad, sets, engine, splits, args.steps, args.warmup)
-    wall = time.perf_counter() - t0
+    wall = []
+    sec = _throughput(pad, sets, engine, splits, args.steps, args.warmup, wall)
     value = nbytes / sec / 1e9
+    trace_us, trace_src = _kernel_trace_us(probe.name)
     traffic, traffic_src = _traffic(probe.name)
 
     result = {
@@ -471,8 +501,9 @@ def main():
             "traffic_source": traffic_src,
             "fetch_gbs": round(traffic / sec / 1e9, 1) if traffic else None,
             "us_per_call": round(sec * 1e6, 3),
-            "kernel_trace_us": _kernel_trace_us(probe.name),
-            "timed_region_wall_s": round(wall, 4),
+            "kernel_trace_us_committed": trace_us,
+            "kernel_trace_source": trace_src,
+            "timed_region_wall_s": round(wall[0], 6),
         },
     }
     if not args.no_ceiling:
@@ -526,12 +557,13 @@ def main():
         sweep = {}
         for b in wl.C2_BATCHES:
             w = wl.make("C2", batch=b, seed=2000 + b)
-            lat = _latency_reference_method(pad, w, engine, splits, args.trials)
+            lat, lat_samples = _latency_reference_method(pad, w, engine, splits, args.trials)
             rs = [w] + _make_sets(wl.make, _rotation(w.k_cache.numel() * 4) - 1, name="C2", batch=b)
             cold = _throughput(pad, rs, engine, splits, args.sweep_calls, 20)
             nb = wl.bytes_of(w)
             sweep[str(b)] = {
                 "us_per_call_warm": round(lat, 2),
+                "us_per_call_warm_trials": [round(x, 2) for x in lat_samples],
                 "us_per_call_cold_throughput": round(cold * 1e6, 2),
                 "gbs_cold": round(nb / cold / 1e9, 1),
                 "pct_of_peak_cold": round(100 * nb / cold / 1e9 / PEAK_GBS, 2),
@@ -544,7 +576,7 @@ def main():
         result["c2_sweep"] = sweep
 
     # Before the headline's CPU baseline: its timings are all GPU ones first.
-    if args.cpu_configs:
+    if args.cpu_configs and args.cpu_configs != "none" and not args.no_cpu:
         recs, table = _cpu_configs(pad, wl, [s for s in args.cpu_configs.split(",") if s], engine, splits,
                                    args.cpu_threads)
         result["cpu_baseline_configs"] = recs

@@ -172,9 +172,8 @@ int pad_decode_counters_needed(const pad_decode_dims* dims, int num_splits,
 /* pad_decode_launch() without workspace or counters arguments: it allocates
  * nothing (no hipMalloc/hipFree, no allocating library call), for callers
  * that cannot allocate - code under HIP graph capture, tight serving loops,
- * harnesses that forbid allocation.  No counterpart in the reference (its
- * launcher allocated the partials on every call,
- * cuda/kernel_v4_split_k.cu:228-232).  The split scratch is a static device
+ * harnesses that forbid allocation.  No counterpart in the reference.  The
+ * split scratch is a static device
  * array of the library, one per GPU, of PAD_NOALLOC_WORKSPACE_BYTES bytes of
  * partials and PAD_NOALLOC_COUNTERS counters; a call whose plan
  * (pad_decode_workspace_bytes() / pad_decode_counters_needed()) needs more
@@ -190,7 +189,8 @@ int pad_decode_launch_noalloc(const void* q, const void* k_cache,
                               const pad_decode_dims* dims, float scale,
                               int num_splits, void* stream);
 
-/* Zero `num_counters` counters (asynchronously, on `stream`); needed once
+/* Zero `num_counters` counters (asynchronously, on `stream`, with a fill
+ * kernel, so a call under stream capture records a kernel node); needed once
  * per counter buffer. */
 int pad_decode_counters_init(int32_t* counters, int64_t num_counters,
                              void* stream);

@@ -1048,7 +1048,8 @@ __device__ __forceinline__ void plan_counts(const Phase1Args& a, const SeqTable<
 
 template <int NK>
 __device__ WorkItem plan_item(const Phase1Args& a, const SeqTable<NK>& t, int g, int G, int lane) {
-  WorkItem w;
+  WorkItem w{};  // a slot without an item keeps defined (zero) fields
+  w.ids_row = a.bt;
   int tot = 0, pmax = 0;
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
@@ -1169,7 +1170,11 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, const SeqR
       w.p_end = a.max_pages;
       w.L = seq_lane_value<NK>(t.len, w.b);
       w.nsplit = a.max_pages > 0 ? 1 : 0;
-      w.slot0 = u;
+      // The item is its unit's only one, so it writes the output rows and
+      // never a partial: its slot is the workgroup's own (g, which the work
+      // list's record check expects), not the unit index, which differs from
+      // g under pair_heads.
+      w.slot0 = g;
       w.col_max = a.max_pages - 1;
       w.valid = (paired ? lin : g) < units;
       w.ids_row = a.bt + (int64_t)w.b * a.sbb;
@@ -1318,6 +1323,9 @@ __global__ __launch_bounds__(64) void pad_plan_kernel(const Phase1Args a, int32_
     case 9: v = a.csr ? (int)(it.ids_row - a.bt) : 0; break;
     default: break;
   }
+  // A slot without an item gets an all-zero record (valid = 0), so lists
+  // planned from the same inputs are identical word for word.
+  if (!it.valid) v = 0;
   // The first page id of wave w's first block, as the decode kernel's
   // first_page_id() reads it (whole-page blocks only).
   const int w = lane - 16;
@@ -1327,7 +1335,7 @@ __global__ __launch_bounds__(64) void pad_plan_kernel(const Phase1Args a, int32_
   }
   int32_t* r = wl + kWlHeaderInts + (int64_t)kWlRecordInts * g;
   if (lane < kWlRecordInts) r[lane] = v;
-  if (g == 0 && lane < 3) wl[lane] = lane == 0 ? kWlMagic : (lane == 1 ? a.wl_key : G);
+  if (g == 0 && lane < kWlHeaderInts) wl[lane] = lane == 0 ? kWlMagic : (lane == 1 ? a.wl_key : (lane == 2 ? G : 0));
 }
 
 // Phase 1: one workgroup per (split, kv head, sequence).
@@ -2165,10 +2173,12 @@ int pad_decode_launch_worklist_csr(const void* q, const void* k_cache, const voi
 int pad_decode_counters_init(int32_t* counters, int64_t num_counters, void* stream) {
   if (!counters) return PAD_ERR_NULL_POINTER;
   if (num_counters <= 0) return PAD_OK;
-  return hipMemsetAsync(counters, 0, (size_t)num_counters * sizeof(int32_t), reinterpret_cast<hipStream_t>(stream)) ==
-                 hipSuccess
-             ? PAD_OK
-             : PAD_ERR_LAUNCH;
+  // A fill kernel, not hipMemsetAsync: under stream capture this records a
+  // kernel node, which replays correctly.
+  const int64_t blocks = (num_counters + 255) / 256;
+  hipLaunchKernelGGL(pad::pad_zero_i32_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), counters, num_counters);
+  return hipGetLastError() == hipSuccess ? PAD_OK : PAD_ERR_LAUNCH;
 }
 
 int pad_device_num_cus(int* num_cus) {

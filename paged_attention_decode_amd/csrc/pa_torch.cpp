@@ -121,9 +121,9 @@ void fill_dims(const torch::Tensor& q, const torch::Tensor& k, const torch::Tens
   for (int i = 0; i < 3; ++i) d->out_stride[i] = out.stride(i);
 }
 
-torch::Tensor forward_impl(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
-                           torch::Tensor block_table, torch::Tensor seq_lens, double scale,
-                           int64_t num_splits, int64_t engine, void* const* events) {
+torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                      torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                      int64_t num_splits, int64_t engine) {
   TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && block_table.is_cuda() &&
                   seq_lens.is_cuda(),
               "pa_decode: all tensors must be on the GPU");
@@ -163,25 +163,9 @@ torch::Tensor forward_impl(torch::Tensor q, torch::Tensor k_cache, torch::Tensor
   st = pad_decode_launch_ex(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                             block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
                             ws_ptr, plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
-                            static_cast<int>(num_splits), static_cast<int>(engine), events, stream);
+                            static_cast<int>(num_splits), static_cast<int>(engine), nullptr, stream);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   return out;
-}
-
-torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
-                      torch::Tensor block_table, torch::Tensor seq_lens, double scale,
-                      int64_t num_splits, int64_t engine) {
-  return forward_impl(q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, engine, nullptr);
-}
-
-// forward() that also records three hipEvent_t handles (raw handles as
-// integers, e.g. torch.cuda.Event.cuda_event): before the kernel, after it,
-// and at the end of the call.
-torch::Tensor forward_events(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
-                             torch::Tensor block_table, torch::Tensor seq_lens, double scale,
-                             int64_t num_splits, int64_t engine, int64_t ev0, int64_t ev1, int64_t ev2) {
-  void* evs[3] = {reinterpret_cast<void*>(ev0), reinterpret_cast<void*>(ev1), reinterpret_cast<void*>(ev2)};
-  return forward_impl(q, k_cache, v_cache, block_table, seq_lens, scale, num_splits, engine, evs);
 }
 
 // Decode with a CSR page index: the page ids of sequence b are
@@ -476,8 +460,6 @@ py::dict plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward", &forward, "Paged-attention decode (q, k_cache, v_cache, block_table, seq_lens, scale, "
                              "num_splits, engine) -> out");
-  m.def("forward_events", &forward_events,
-        "forward() recording three hipEvent_t handles: before phase 1, after phase 1, after phase 2");
   m.def("forward_v4", &forward_v4, "Paged-attention decode with the reference forward_v4 argument list");
   m.def("forward_csr", &forward_csr,
         "Paged-attention decode over a CSR page index (q, k_cache, v_cache, indptr, indices, last_page_len, "

@@ -51,3 +51,24 @@ def test_row_subset_with_an_empty_row():
     full = paged_attention_decode_reference(w.q.float(), w.k_cache.float(), w.v_cache.float(), w.block_table,
                                             w.seq_lens, w.scale)
     torch.testing.assert_close(out[0], full[0], rtol=0, atol=0)
+
+
+def test_committed_kernel_trace_is_labelled_with_its_source():
+    bench = _bench()
+    us, src = bench._kernel_trace_us("C2_b64")
+    assert us is not None and us > 0
+    assert "profiles/pad_phase1_kernel_configs_kernel_trace.txt" in src and "commit" in src
+    assert bench._kernel_trace_us("no_such_config") == (None, None)
+
+
+def test_per_config_cpu_baseline_is_on_by_default():
+    import sys
+
+    bench = _bench()
+    argv = sys.argv
+    try:
+        sys.argv = ["bench.py"]
+        args = bench._parse()
+    finally:
+        sys.argv = argv
+    assert set(args.cpu_configs.split(",")) >= {"C1", "C3", "C4"}

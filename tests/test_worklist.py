@@ -94,6 +94,11 @@ GPU_CASES = [
     ("ragged100", 4, 4, 128, 16, None),
     ("oversub", 2, 6, 128, 16, None),
     ("oversub_full", 2, 6, 128, 16, None),
+    # head_dim 96 and 32 with an even kv-head count: kv heads paired on an
+    # XCD (grid_pos), so a workgroup's index differs from its unit's
+    ("oversub_full", 2, 6, 96, 16, None),
+    ("oversub_full", 2, 4, 32, 16, None),
+    ("oversub", 2, 6, 96, 16, None),
     ("full16", 2, 6, 128, 16, None),
     ("empty", 2, 6, 128, 16, None),
     ("empty", 2, 6, 64, 8, None),  # sub-page blocks
@@ -300,29 +305,39 @@ def _check_plan_structure(wl, lens, ps, hkv, bt_rows, nw, max_pages):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("kind,ps,csr", [("ragged32", 32, False), ("ragged100", 16, False), ("oversub", 16, False),
-                                         ("full16", 16, False), ("empty", 16, False), ("allempty", 16, False),
-                                         ("ragged32", 32, True), ("empty", 8, True)])
-def test_work_list_covers_every_page_once(kind, ps, csr):
+@pytest.mark.parametrize("kind,ps,csr,d", [("ragged32", 32, False, 128), ("ragged100", 16, False, 128),
+                                           ("oversub", 16, False, 128), ("full16", 16, False, 128),
+                                           ("empty", 16, False, 128), ("allempty", 16, False, 128),
+                                           ("ragged32", 32, True, 128), ("empty", 8, True, 128),
+                                           ("oversub_full", 16, False, 96), ("oversub_full", 16, False, 32),
+                                           ("oversub", 16, False, 96), ("ragged32", 32, False, 96)])
+def test_work_list_covers_every_page_once(kind, ps, csr, d):
     import paged_attention_decode_amd as pad
     from paged_attention_decode_amd._native import ext
 
     lens, seed = _lens(kind, 31)
     hkv, group = 2, 6
-    q, k, v, bt, sl = _dense_case(lens, hkv, group, 128, ps, seed)
+    q, k, v, bt, sl = _dense_case(lens, hkv, group, d, ps, seed)
     if csr:
         indptr, indices, last = pad.paged_kv_indices(bt, sl, ps)
-        wl = ext().plan_worklist_csr(indptr, indices, last, hkv * group, hkv, 128, ps, 0)
+        plan = lambda: ext().plan_worklist_csr(indptr, indices, last, hkv * group, hkv, d, ps, 0)  # noqa: E731
         ip = indptr.cpu().tolist()
         rows = [indices.cpu()[ip[b]:ip[b + 1]].tolist() for b in range(len(lens))]
         max_pages = 1 << 30
-        nw = pad.plan(len(lens), hkv * group, hkv, 128, ps, max(indices.numel(), 1), csr=True)["waves_per_group"]
+        nw = pad.plan(len(lens), hkv * group, hkv, d, ps, max(indices.numel(), 1), csr=True)["waves_per_group"]
     else:
-        wl = ext().plan_worklist(bt, sl, hkv * group, hkv, 128, ps, 0)
+        plan = lambda: ext().plan_worklist(bt, sl, hkv * group, hkv, d, ps, 0)  # noqa: E731
         rows = bt.cpu().tolist()
         max_pages = bt.shape[1]
-        nw = pad.plan(len(lens), hkv * group, hkv, 128, ps, max_pages)["waves_per_group"]
+        nw = pad.plan(len(lens), hkv * group, hkv, d, ps, max_pages)["waves_per_group"]
+    wl = plan()
+    # Planning the same inputs again (into fresh memory) gives the same list
+    # word for word, including the records of slots without an item.
+    junk = torch.full((wl.numel(),), 0x5A, dtype=torch.uint8, device="cuda")
+    del junk
+    wl2 = plan()
     torch.cuda.synchronize()
+    assert torch.equal(wl, wl2)
     _check_plan_structure(wl.cpu().view(torch.int32), lens, ps, hkv, rows, nw, max_pages)
 
 
