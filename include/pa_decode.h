@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PAD_ABI_VERSION 5
+#define PAD_ABI_VERSION 4
 
 /* Largest supported GQA group (query heads per KV head); the reference's
  * bound is the same (cuda/kernel_v4_split_k.cu:44). */
@@ -116,9 +116,7 @@ typedef struct pad_decode_plan_t {
   int32_t waves_per_group;  /* 64-lane waves per phase-1 workgroup         */
   int32_t single_pass;      /* 1: one split per sequence, no partials      */
   int32_t engine;           /* 0 = MFMA tiles, 1 = VALU/DPP dot products   */
-  int32_t slots_per_group;  /* workspace slots per workgroup: 2 when ragged
-                               lengths may give a workgroup two stream
-                               items (ranges that span two units), else 1  */
+  int32_t reserved;
   size_t workspace_bytes;   /* fp32 partials; 0 if single_pass             */
   int64_t counters;         /* int32 arrival counters; 0 if single_pass    */
 } pad_decode_plan_t;

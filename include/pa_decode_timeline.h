@@ -46,7 +46,6 @@ extern "C" {
 #define PAD_TL_F_SINGLE 2   /* the unit had one item: no partials, no merge  */
 #define PAD_TL_F_MERGER 4   /* last arrival of its unit                       */
 #define PAD_TL_F_GROUP 8    /* last arrival of a two-level merge group        */
-#define PAD_TL_F_TWO 16     /* the workgroup held two stream items            */
 
 /* Copy the stamp buffer (at most `bytes`) to host memory; synchronous. */
 int pad_timeline_read(void* host, size_t bytes);

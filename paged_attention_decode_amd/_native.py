@@ -77,7 +77,7 @@ class PadPlan(ctypes.Structure):
         ("waves_per_group", ctypes.c_int32),
         ("single_pass", ctypes.c_int32),
         ("engine", ctypes.c_int32),
-        ("slots_per_group", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_size_t),
         ("counters", ctypes.c_int64),
     ]
@@ -162,7 +162,7 @@ TIMELINE_SIGNATURES = {
 # include/pa_decode_timeline.h
 TL_LAUNCHES, TL_MAX_GROUPS, TL_SLOTS = 4, 16384, 8
 TL_ENTRY, TL_ITEM, TL_LOOP_END, TL_PUBLISHED, TL_ARRIVED, TL_MERGED, TL_EXIT, TL_INFO = range(8)
-TL_F_NO_ITEM, TL_F_SINGLE, TL_F_MERGER, TL_F_GROUP, TL_F_TWO = 1, 2, 4, 8, 16
+TL_F_NO_ITEM, TL_F_SINGLE, TL_F_MERGER, TL_F_GROUP = 1, 2, 4, 8
 _timeline = None
 
 

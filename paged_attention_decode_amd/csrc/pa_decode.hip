@@ -119,7 +119,6 @@ struct Phase1Args {
   int min_chunk;   // planner: fewest pages per item
   int pair_heads;  // 1: workgroups 8 apart take kv heads 2m and 2m+1 (see grid_pos)
   int wl_key;      // key of the launch's plan, matched against the work list's header
-  int stream;      // 1: the stream kernel (stream items, two workspace slots per workgroup)
   float scale_log2;
   const int32_t* bt;      // dense: block_table [B, max_pages]; CSR: indices
   const int32_t* sl;      // dense: seq_lens [B]
@@ -286,16 +285,14 @@ template <int N>
 struct MergeBatch {
   float2 ml[N];
   f4_t o[N];
-  // Entry e = sp0 + j sits in slot e * stride of the region, entry 0 in
-  // slot `odd` (stream items: the unit may start inside a workgroup's range).
+  // Entry sp0 + j sits in split slot (sp0 + j) * stride.
   __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t o_rsrc, __amdgpu_buffer_rsrc_t ml_rsrc, int sp0,
-                                       int stride, int odd, int gqa, int row, int col, int d) {
-    auto slot = [&](int j) { return (sp0 + j) * stride + (sp0 + j == 0 ? odd : 0); };
+                                       int stride, int gqa, int row, int col, int d) {
 #pragma unroll
-    for (int j = 0; j < N; ++j) ml[j] = load_device_f2(ml_rsrc, (uint32_t)(slot(j) * gqa + row) * 8u);
+    for (int j = 0; j < N; ++j) ml[j] = load_device_f2(ml_rsrc, (uint32_t)((sp0 + j) * stride * gqa + row) * 8u);
 #pragma unroll
     for (int j = 0; j < N; ++j)
-      o[j] = load_device_f4(o_rsrc, ((uint32_t)(slot(j) * gqa + row) * (uint32_t)d + col) * 4u);
+      o[j] = load_device_f4(o_rsrc, ((uint32_t)((sp0 + j) * stride * gqa + row) * (uint32_t)d + col) * 4u);
   }
   // Entries at or past `end` fold with m_s = -inf, i.e. weight 0 (their
   // loads read zeros: they lie past the unit's region): the fold has no
@@ -317,31 +314,29 @@ struct MergeBatch {
   }
 };
 
-// Folds entries [first, first + count) of one element (entry i in slot
-// i * stride, entry 0 in slot `odd`), one memory round trip per batch: 4, 8
-// or 16 entries for counts up to 4, 8 and 16, batches of 16 beyond.  Entries
-// a batch reads past the count must lie past the unit's region (they read
-// zeros).
+// Folds entries [first, first + count) of one element (entry i in split
+// slot i * stride), one memory round trip per batch: 4, 8 or 16 entries for
+// counts up to 4, 8 and 16, batches of 16 beyond.  Entries a batch reads
+// past the count must lie past the unit's region (they read zeros).
 __device__ __forceinline__ void merge_partials(__amdgpu_buffer_rsrc_t o_rsrc, __amdgpu_buffer_rsrc_t ml_rsrc,
-                                               int first, int count, int stride, int odd, int gqa, int row, int col,
-                                               int d, float& m, float& l, f4_t& acc) {
+                                               int first, int count, int stride, int gqa, int row, int col, int d,
+                                               float& m, float& l, f4_t& acc) {
   const int end = first + count;
   if (count <= 4) {
     MergeBatch<4> p;
-    p.load(o_rsrc, ml_rsrc, first, stride, odd, gqa, row, col, d);
+    p.load(o_rsrc, ml_rsrc, first, stride, gqa, row, col, d);
     p.fold(first, end, m, l, acc);
     return;
   }
   if (count <= 8) {
     MergeBatch<8> p;
-    p.load(o_rsrc, ml_rsrc, first, stride, odd, gqa, row, col, d);
+    p.load(o_rsrc, ml_rsrc, first, stride, gqa, row, col, d);
     p.fold(first, end, m, l, acc);
     return;
   }
-
   for (int sp0 = first; sp0 < end; sp0 += 16) {
     MergeBatch<16> p;
-    p.load(o_rsrc, ml_rsrc, sp0, stride, odd, gqa, row, col, d);
+    p.load(o_rsrc, ml_rsrc, sp0, stride, gqa, row, col, d);
     p.fold(sp0, end, m, l, acc);
   }
 }
@@ -417,38 +412,11 @@ constexpr int kModeSubpage = 2;
 template <int D>
 constexpr bool q_in_lds() { return D >= 256; }
 
-// The item after this one (stream kernel: item 2 of a workgroup), whose
-// first tile each wave issues ahead, while its last tiles of this item are
-// computed (nblk 0: none).
-struct NextItem {
-  const int32_t* ids_row;
-  int64_t ids_stride;
-  int b, kvh, t_begin, nblk, phys_first;
-};
-
-// A wave's first tile of the next item issued ahead: its K/V registers (in
-// flight), its Q^T operand and the raw page id of its second block (a
-// scalar load in flight).
-template <int D>
-struct TileAhead {
-  KVTile<D> t;
-  h8_t q[D / 32];
-  int pid_next;
-};
-
-// AHEAD_IN: the wave's first block and q are already in *ah (issued by the
-// previous item's loop); AHEAD_OUT: issue the first block and q of *nx into
-// *ah once this item has at most two blocks left for the wave (or none), so
-// the wave's load pipeline does not drain between the two items: a drained
-// pipeline costs a loaded memory latency, ~2 us at full bandwidth.
-template <int D, int MODE, bool AHEAD_IN = false, bool AHEAD_OUT = false>
+template <int D, int MODE>
 __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_first, const int32_t* bt_row,
                                                int64_t ids_stride, int b, int kvh, int t_begin, int t_end,
                                                int nblk, int wave, int nw, int lane, float2* sm_ml, float* sm_o,
-                                               char* k_stage, char* q_stage, TileAhead<D>* ah = nullptr,
-                                               const NextItem* nx = nullptr) {
-  static_assert(!(AHEAD_IN || AHEAD_OUT) || (MODE == kModeUniform && !q_in_lds<D>()),
-                "tiles issued ahead: whole-page blocks and q in registers only");
+                                               char* k_stage, char* q_stage) {
   constexpr int DK = D / 32;  // 16-byte K chunks per lane per token
   constexpr int DT = D / 16;  // PV output tiles; V halves per lane per token
   constexpr int NDW = DT / 2;
@@ -480,13 +448,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   const bool row_ok = r16 < a.gqa;
   // The wave's Q^T operand (B of S^T = K.Q^T: row r16, head_dim slots
   // kp*32 + g*8 + [0,8)), loaded after the first K/V block is in flight.
-  h8_t qv_own[q_in_lds<D>() ? 1 : DK];
-  auto& qv = [&]() -> auto& {
-    if constexpr (AHEAD_IN)
-      return ah->q;
-    else
-      return qv_own;
-  }();
+  h8_t qv[q_in_lds<D>() ? 1 : DK];
   auto q_slot = [&](int kp) -> h8_t* {
     return reinterpret_cast<h8_t*>(q_stage + r16 * k_stage_row_bytes<D>() + (kp * 32 + g * 8) * 2);
   };
@@ -566,12 +528,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   // consumes it and issues the scalar read of the following block's id, so
   // that read is in flight during a whole compute() (calls come in block
   // order wave, wave+nw, ...; past the split the last block's id is reread).
-  // With the first block issued ahead, the next load() reads the second.
-  int pid_next;
-  if constexpr (AHEAD_IN)
-    pid_next = ah->pid_next;
-  else
-    pid_next = phys_first;
+  int pid_next = phys_first;
 
   auto load = [&](KVTile<D>& t, int jb) {
     if constexpr (MODE == kModeUniform) {
@@ -717,55 +674,17 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
     }
   };
 
-  // The next item's first block and q for this wave, issued into *ah (the
-  // uniform-mode load() for block `wave` of that item).
-  auto issue_ahead = [&]() {
-    if constexpr (AHEAD_OUT) {
-      if (wave < nx->nblk) {
-        const char* k_next = reinterpret_cast<const char*>(a.k + (int64_t)nx->kvh * a.skh);
-        const char* v_next = reinterpret_cast<const char*>(a.v + (int64_t)nx->kvh * a.svh);
-        const int p_next = page_of(a, nx->t_begin);
-        const int jp = block_page(a, wave);
-        const int slot0 = wave * kBlockTokens - jp * a.ps;
-        const int phys = clamp_page(nx->phys_first, a.num_pages);
-        const int page_after = p_next + block_page(a, min(wave + nw, nx->nblk - 1));
-        ah->pid_next = load_uniform_i32(nx->ids_row + (int64_t)page_after * nx->ids_stride);
-        const char* kb = k_next + ((int64_t)phys * a.skp + (int64_t)slot0 * a.sks) * 2;
-        const char* vb = v_next + ((int64_t)phys * a.svp + (int64_t)slot0 * a.svs) * 2;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ah->t.k[i] = load_slice(kb + koff[i]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ah->t.v[i] = load_slice(vb + voff[i]);
-        const _Float16* qrow =
-            a.q + (int64_t)nx->b * a.sqb + (int64_t)(nx->kvh * a.gqa + (row_ok ? r16 : 0)) * a.sqh;
-#pragma unroll
-        for (int kp = 0; kp < DK; ++kp) {
-          const h8_t x = *reinterpret_cast<const h8_t*>(qrow + kp * 32 + g * 8);
-          ah->q[kp] = row_ok ? x : (h8_t)0;
-        }
-      }
-    }
-  };
-
   // This wave's blocks are wave, wave+nw, ...  The steady-state loop issues
   // the next block's loads unconditionally before computing the current one
   // (no control-flow join on the in-flight registers); the last one or two
   // blocks are peeled.
   const int n_mine = wave < nblk ? (nblk - wave + nw - 1) / nw : 0;
-  KVTile<D> ta_own, tb;
-  auto& ta = [&]() -> KVTile<D>& {
-    if constexpr (AHEAD_IN)
-      return ah->t;
-    else
-      return ta_own;
-  }();
+  KVTile<D> ta, tb;
   if (n_mine > 0) {
     int it = 0;
-    if constexpr (!AHEAD_IN) {
-      fetch_ids(wave);
-      load(ta, wave);
-      load_q();
-    }
+    fetch_ids(wave);
+    load(ta, wave);
+    load_q();
     for (; it + 2 < n_mine; it += 2) {
       load(tb, wave + (it + 1) * nw);
       compute(ta, wave + it * nw);
@@ -774,15 +693,11 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
     }
     if (it + 1 < n_mine) {
       load(tb, wave + (it + 1) * nw);
-      issue_ahead();
       compute(ta, wave + it * nw);
       compute(tb, wave + (it + 1) * nw);
     } else {
-      issue_ahead();
       compute(ta, wave + it * nw);
     }
-  } else {
-    issue_ahead();
   }
 
   // Row totals: the four 16-lane groups hold disjoint token subsets.
@@ -965,16 +880,9 @@ struct WorkItem {
   int p_begin, p_end;  // logical pages [p_begin, p_end) of sequence b
   int L;               // tokens of sequence b
   int nsplit;          // items of the unit; 0: the unit is empty (write zeros)
-  int slot0;           // workspace slot the unit's partials are addressed from
+  int slot0;           // workspace slot of the unit's first item
   int col_max;         // last page-id column that may be read speculatively
   int valid;           // 0: no item for this workgroup
-  // Where the unit's items keep their partials: item e of the unit in slot
-  // slot0 + sstride * e, plus odd for e = 0; this item's own slot is `slot`.
-  // Per-unit items: consecutive slots (sstride 1, odd 0, slot = g).
-  // Stream items (two slots per workgroup, see plan_stream): sstride 2.
-  int slot;
-  int sstride;
-  int odd;
   const int32_t* ids_row;
   int64_t ids_stride;
 };
@@ -1142,8 +1050,6 @@ template <int NK>
 __device__ WorkItem plan_item(const Phase1Args& a, const SeqTable<NK>& t, int g, int G, int lane) {
   WorkItem w{};  // a slot without an item keeps defined (zero) fields
   w.ids_row = a.bt;
-  w.slot = g;
-  w.sstride = 1;
   int tot = 0, pmax = 0;
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
@@ -1212,146 +1118,6 @@ __device__ WorkItem plan_item(const Phase1Args& a, const SeqTable<NK>& t, int g,
   return w;
 }
 
-// floor(x / y) for 0 <= x < 2^50 and 0 < y < 2^31 (ry = 1 / y): the double
-// estimate is within one of the quotient, exact integer products correct it.
-__device__ __forceinline__ int64_t floor_div_i64(int64_t x, int64_t y, double ry) {
-  int64_t q = (int64_t)((double)x * ry);
-  q -= q * y > x ? 1 : 0;
-  q += (q + 1) * y <= x ? 1 : 0;
-  return q;
-}
-
-// Stream items (the launches of the stream kernel; heuristic split count):
-// the units' pages, laid end to end in (sequence, kv head) order, are cut
-// into G ranges of equal length (to one page), one per workgroup, so that
-// every workgroup streams the same number of pages whatever the lengths.
-// (Per-unit chunks leave each unit's last chunk short, and the chunk must
-// grow until the units fit the grid: on ragged 32-sequence batches the
-// longest item ran ~1.2x the mean.)
-//
-// Each unit counts as max(pages, T) virtual pages, its real pages first,
-// with T at least the longest range, so no unit lies strictly inside a range:
-// a range holds the tail of one unit (item 1) and at most the head of the
-// next (item 2).  T is the smallest of up to three candidates with
-// W(T) = Hkv * sum_b max(pages_b, T) <= G * T (then every range, of at most
-// ceil(W / G) pages, is no longer than T): ceil(unit pages / G), the fixed
-// point iterate ceil(W / G) from it, else ceil(unit pages / (G - units)),
-// which always qualifies (W <= unit pages + units * T).  Range g covers
-// virtual pages [floor(g W / G), floor((g + 1) W / G)).
-//
-// Workgroup g keeps item 1's partial in slot 2g and item 2's in slot 2g + 1.
-// A unit whose pages meet ranges gf..gl has items in slots 2gf (2gf + 1 when
-// it starts inside range gf, as item 2), 2(gf + 1), ..., 2gl: slot0 = 2gf,
-// sstride 2, odd 0 or 1.  An empty unit's zero rows belong to the range
-// where its virtual pages start.  Returns false (per-unit chunks instead)
-// when the ranges would be shorter than min_chunk pages, or the batch has
-// more than 2^28 unit pages.
-template <int NK>
-__device__ bool plan_stream(const Phase1Args& a, const SeqTable<NK>& t, int g, int G, int lane, WorkItem& w1,
-                            WorkItem& w2) {
-  int tot = 0;
-#pragma unroll
-  for (int k = 0; k < NK; ++k) tot += t.pages[k];
-  tot = wave_sum_i32(tot);
-  const int hkv = a.hkv;
-  const int units = a.batch * hkv;
-  const int64_t up = (int64_t)tot * hkv;
-  if (up < (int64_t)G * a.min_chunk || up > (1 << 28)) return false;
-  const double rG = 1.0 / (double)G;
-  // W(T) <= 2^29 here: sum_b max(pages_b, T) <= tot + batch * T, and every
-  // candidate T is at most unit pages / ((S - 1) Hkv).
-  auto vpages = [&](int T) -> int64_t {
-    int x = 0;
-#pragma unroll
-    for (int k = 0; k < NK; ++k) x += lane + 64 * k < a.batch ? max(t.pages[k], T) : 0;
-    return (int64_t)wave_sum_i32(x) * hkv;
-  };
-  int T = (int)floor_div_i64(up + G - 1, G, rG);
-  int64_t W = vpages(T);
-  if (W > (int64_t)G * T) {
-    const int T1 = (int)floor_div_i64(W + G - 1, G, rG);
-    const int64_t W1 = vpages(T1);
-    if (W1 <= (int64_t)G * T1) {
-      T = T1;
-      W = W1;
-    } else {
-      const int64_t spare = G - units;  // > 0: a planned launch has at least 2 splits
-      T = (int)floor_div_i64(up + spare - 1, spare, 1.0 / (double)spare);
-      W = vpages(T);
-    }
-  }
-  const double rW = 1.0 / (double)W;
-  const int lo = (int)floor_div_i64((int64_t)g * W, G, rG);
-  const int hi = (int)floor_div_i64((int64_t)(g + 1) * W, G, rG);
-  // The range holding virtual page x, and the first page of range r.
-  auto range_of = [&](int x) { return (int)floor_div_i64((int64_t)(x + 1) * G - 1, W, rW); };
-  auto range_lo = [&](int r) { return (int)floor_div_i64((int64_t)r * W, G, rG); };
-
-  // Unit of virtual page lo: sequence b1 from a prefix scan of Hkv * V_b
-  // (V_b = max(pages_b, T)), then its kv head.
-  int carry = 0, b1 = 0, base1 = 0;
-#pragma unroll
-  for (int k = 0; k < NK; ++k) {
-    if (64 * k >= a.batch) break;
-    const bool in = lane + 64 * k < a.batch;
-    const int x = in ? max(t.pages[k], T) * hkv : 0;
-    const int incl = wave_incl_scan_i32(x, lane) + carry;
-    const int excl = incl - x;
-    const uint64_t hit = __builtin_amdgcn_ballot_w64(in && excl <= lo && lo < incl);
-    if (hit != 0) {
-      const int l = (int)__builtin_ctzll(hit);
-      b1 = 64 * k + l;
-      base1 = __builtin_amdgcn_readlane(excl, l);
-      break;
-    }
-    carry = __builtin_amdgcn_readlane(incl, 63);
-  }
-  const int P1 = seq_lane_value<NK>(t.pages, b1);
-  const int V1 = max(P1, T);
-  int h1 = (int)((float)(lo - base1) / (float)V1);  // < Hkv; within one of the quotient
-  h1 -= h1 * V1 > lo - base1 ? 1 : 0;
-  h1 += (h1 + 1) * V1 <= lo - base1 ? 1 : 0;
-  const int s1 = base1 + h1 * V1;  // first virtual page of unit (b1, h1)
-
-  // One item: pages [p_begin, p_end) of unit (b, kvh), whose virtual pages
-  // start at su, in slot `slot`.
-  auto fill = [&](WorkItem& w, int b, int kvh, int su, int p_begin, int p_end, int slot) {
-    const int P = seq_lane_value<NK>(t.pages, b);
-    w.b = b;
-    w.kvh = kvh;
-    w.L = seq_lane_value<NK>(t.len, b);
-    w.p_begin = p_begin;
-    w.p_end = p_end;
-    w.col_max = P - 1;
-    w.valid = 1;
-    w.slot = slot;
-    w.sstride = 2;
-    w.ids_row = a.csr ? a.bt + seq_lane_value<NK>(t.row, b) : a.bt + (int64_t)b * a.sbb;
-    w.ids_stride = a.csr ? 1 : a.sbp;
-    if (P == 0) {  // the unit's zero rows
-      w.nsplit = 0;
-      w.slot0 = slot;
-      w.odd = 0;
-      return;
-    }
-    const int gf = range_of(su);
-    w.nsplit = range_of(su + P - 1) - gf + 1;
-    w.slot0 = 2 * gf;
-    w.odd = range_lo(gf) != su ? 1 : 0;
-  };
-  if (lo - s1 < P1)
-    fill(w1, b1, h1, s1, lo - s1, min(hi - s1, P1), 2 * g);
-  else if (P1 == 0 && lo == s1)
-    fill(w1, b1, h1, s1, 0, 0, 2 * g);
-  const int s2 = s1 + V1;
-  if (s2 < hi) {  // the range ends inside the next unit (it has one: s2 < W)
-    const bool same = h1 + 1 < hkv;
-    const int b2 = same ? b1 : b1 + 1;
-    fill(w2, b2, same ? h1 + 1 : 0, s2, 0, min(hi - s2, seq_lane_value<NK>(t.pages, b2)), 2 * g + 1);
-  }
-  return true;
-}
-
 // The static item of workgroup (s, kvh, b) given the sequence's length and
 // page count.  The dense table splits every row's max_pages columns into
 // num_splits ranges of pps pages; a CSR index has no common row width, so
@@ -1367,9 +1133,6 @@ __device__ __forceinline__ WorkItem static_item(const Phase1Args& a, int s, int 
   w.p_end = min(w.p_begin + pps, pages);
   w.nsplit = (pages + pps - 1) / pps;
   w.slot0 = (b * a.hkv + kvh) * a.num_splits;
-  w.slot = w.slot0 + s;
-  w.sstride = 1;
-  w.odd = 0;
   w.col_max = a.csr ? pages - 1 : a.max_pages - 1;
   // Splits past the sequence's last page do nothing, except split 0 of an
   // empty sequence, which writes its zero rows.
@@ -1383,11 +1146,10 @@ __device__ __forceinline__ WorkItem static_item(const Phase1Args& a, int s, int 
 // capacity the static split is already even (balance == 1) or, on an
 // oversubscribed grid (balance == 2: at least as many (sequence, kv head)
 // units as CUs), each unit is one item of workgroup g = unit and the other
-// workgroups exit; otherwise plan the items: stream items (STREAM, the
-// stream kernel: a second item may come back in it2) or per-unit chunks.
-template <int NK, bool STREAM>
+// workgroups exit; otherwise plan the items.
+template <int NK>
 __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, const SeqRaw& raw, int s, int h, int bz, int g,
-                                                 int G, int lin, const int32_t* static_row, int lane, WorkItem& it2) {
+                                                 int G, int lin, const int32_t* static_row, int lane) {
   const SeqTable<NK> t = seq_table<NK>(a, raw, lane);
   bool full = !a.csr;
 #pragma unroll
@@ -1413,9 +1175,6 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, const SeqR
       // list's record check expects), not the unit index, which differs from
       // g under pair_heads.
       w.slot0 = g;
-      w.slot = g;
-      w.sstride = 1;
-      w.odd = 0;
       w.col_max = a.max_pages - 1;
       w.valid = (paired ? lin : g) < units;
       w.ids_row = a.bt + (int64_t)w.b * a.sbb;
@@ -1424,28 +1183,20 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, const SeqR
     }
     return static_item(a, s, h, bz, seq_lane_value<NK>(t.len, bz), a.max_pages, static_row, a.sbp);
   }
-  if constexpr (STREAM) {
-    WorkItem w1{};
-    w1.ids_row = a.bt;
-    if (plan_stream<NK>(a, t, g, G, lane, w1, it2)) return w1;
-  }
   return plan_item<NK>(a, t, g, G, lane);
 }
 
 // The work item of workgroup (s, h, bz) = slot g: the in-kernel plan when
-// a.balance is set, else the static split; with STREAM a second item (of
-// stream items) in it2, which the caller passes in without an item
-// (value-initialised).  raw is issue_seq_table()'s loads; static_len is
-// seq_lens[bz] (dense) or any word (CSR).  The decode kernel and the
-// work-list planner both call this, so a planned launch runs exactly the
-// items of an unplanned one.
-template <bool STREAM>
+// a.balance is set, else the static split.  raw is issue_seq_table()'s
+// loads; static_len is seq_lens[bz] (dense) or any word (CSR).  The decode
+// kernel and the work-list planner both call this, so a planned launch runs
+// exactly the items of an unplanned one.
 __device__ __forceinline__ WorkItem resolve_workgroup(const Phase1Args& a, const SeqRaw& raw, int s, int h, int bz,
                                                       int g, int G, int lin, const int32_t* static_row,
-                                                      int static_len, int lane, WorkItem& it2) {
+                                                      int static_len, int lane) {
   if (a.balance) {
-    if (a.batch <= 64) return resolve_item<1, STREAM>(a, raw, s, h, bz, g, G, lin, static_row, lane, it2);
-    return resolve_item<4, STREAM>(a, raw, s, h, bz, g, G, lin, static_row, lane, it2);
+    if (a.batch <= 64) return resolve_item<1>(a, raw, s, h, bz, g, G, lin, static_row, lane);
+    return resolve_item<4>(a, raw, s, h, bz, g, G, lin, static_row, lane);
   }
   if (a.csr) {
     int row, pages, L;
@@ -1457,28 +1208,35 @@ __device__ __forceinline__ WorkItem resolve_workgroup(const Phase1Args& a, const
 }
 
 // Work list (pad_decode_plan_worklist): a header of kWlHeaderInts int32
-// {magic, plan key, G, 0...} and one record of kWlRecordInts int32 per
-// workgroup g: two halves of kWlItemInts, item 1 and item 2 (item 2 only in
-// stream launches, else all zero), each {b, kvh, p_begin, p_end, L, nsplit,
-// slot0, col_max, valid, row (CSR offset of the sequence's ids, else 0),
-// slot, sstride, odd, 3 unused, then the raw page id of the first block of
-// waves 0-7 (whole-page blocks; 0 otherwise), 8 unused}.  A half without an
-// item is all zero.
+// {magic, plan key, G} and one record of kWlRecordInts int32 per workgroup
+// slot g: {b, kvh, p_begin, p_end, L, nsplit, slot0, col_max, valid, row
+// (CSR offset of the sequence's ids, else 0), 6 unused, then the raw page id
+// of the first block of waves 0-7 (whole-page blocks; 0 otherwise), 8
+// unused}.
 constexpr int kWlHeaderInts = 32;
-constexpr int kWlItemInts = 32;
-constexpr int kWlRecordInts = 2 * kWlItemInts;
-constexpr int kWlItemFields = 13;
-constexpr int kWlPidWord = 16;
+constexpr int kWlRecordInts = 32;
 constexpr int kWlMagic = 0x574c4150;  // "PALW"
 
-// Half `half` of workgroup g's record (its fields f) as a work item.  The
-// item must own its workgroup's slot: g for per-unit items (sstride 1, half
-// 0 only; slots [0, G)), 2g + half for stream items (sstride 2, stream
-// launches only; slots [0, 2G)).  A record that does not describe an item of
-// this launch's shapes is treated as no item, so a stale list can give
-// wrong rows but never reads or writes out of bounds.
-__device__ __forceinline__ void worklist_decode(const Phase1Args& a, const int (&f)[kWlItemFields], int g, int G,
-                                                int half, int max_sstride, WorkItem& w) {
+// Record g of a.worklist as a work item and the raw first page id of this
+// wave's first block.  False (use the in-kernel plan) when the header does
+// not carry this launch's plan key.  A record that does not describe an
+// item of this launch's shapes is treated as no item, so a stale list can
+// give wrong rows but never reads or writes out of bounds.
+__device__ __forceinline__ bool worklist_item(const Phase1Args& a, int g, int G, int wave, WorkItem& w, int& pid) {
+  const int32_t* r = a.worklist + kWlHeaderInts + (int64_t)kWlRecordInts * g;
+  const int magic = load_uniform_i32(a.worklist);
+  const int key = load_uniform_i32(a.worklist + 1);
+  int f[10];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) f[i] = load_uniform_i32(r + i);
+  pid = load_uniform_i32(r + 16 + wave);
+  // The record's values are only used past the header check, so the
+  // compiler would sink their loads below it: a second round trip.  Pinning
+  // them here keeps the header and the record in one.
+#pragma unroll
+  for (int i = 0; i < 10; ++i) asm volatile("" : "+s"(f[i]));
+  asm volatile("" : "+s"(pid));
+  if (magic != kWlMagic || key != a.wl_key) return false;
   w.b = f[0];
   w.kvh = f[1];
   w.p_begin = f[2];
@@ -1488,72 +1246,23 @@ __device__ __forceinline__ void worklist_decode(const Phase1Args& a, const int (
   w.slot0 = f[6];
   w.col_max = f[7];
   const int row = f[9];
-  w.slot = f[10];
-  w.sstride = f[11];
-  w.odd = f[12];
-  const bool stream_item = w.sstride == 2 && max_sstride == 2;
-  const int my_slot = stream_item ? 2 * g + half : g;
-  const int slots = stream_item ? 2 * G : G;
   const bool ok = f[8] != 0 && w.b >= 0 && w.b < a.batch && w.kvh >= 0 && w.kvh < a.hkv && w.p_begin >= 0 &&
                   w.p_begin <= w.p_end && w.p_end <= w.col_max + 1 && w.L >= 0 && w.nsplit >= 0 &&
-                  w.nsplit <= slots && (stream_item || (w.sstride == 1 && half == 0)) && w.odd >= 0 &&
-                  w.odd < w.sstride && w.slot == my_slot && w.slot0 >= 0 &&
-                  (int64_t)w.slot0 + (int64_t)w.sstride * w.nsplit <= slots &&
-                  (w.nsplit == 0 || (w.slot >= w.slot0 && w.slot < w.slot0 + w.sstride * w.nsplit)) && row >= 0 &&
+                  w.nsplit <= G && w.slot0 >= 0 && w.slot0 <= G - w.nsplit &&
+                  (w.nsplit == 0 || (g >= w.slot0 && g < w.slot0 + w.nsplit)) && row >= 0 &&
                   (int64_t)row + w.col_max < a.max_pages;
   w.valid = ok ? 1 : 0;
   w.ids_row = a.csr ? a.bt + row : a.bt + (int64_t)(ok ? w.b : 0) * a.sbb;
   w.ids_stride = a.csr ? 1 : a.sbp;
-}
-
-// Record g of a.worklist as work items and the raw first page id of this
-// wave's first block of each (item 2 only with STREAM).  False (use the
-// in-kernel plan) when the header does not carry this launch's plan key.
-template <bool STREAM>
-__device__ __forceinline__ bool worklist_item(const Phase1Args& a, int g, int G, int wave, WorkItem& w, int& pid,
-                                              WorkItem& w2, int& pid2) {
-  const int32_t* r = a.worklist + kWlHeaderInts + (int64_t)kWlRecordInts * g;
-  const int magic = load_uniform_i32(a.worklist);
-  const int key = load_uniform_i32(a.worklist + 1);
-  int f[kWlItemFields], f2[kWlItemFields];
-#pragma unroll
-  for (int i = 0; i < kWlItemFields; ++i) f[i] = load_uniform_i32(r + i);
-  pid = load_uniform_i32(r + kWlPidWord + wave);
-  if constexpr (STREAM) {
-#pragma unroll
-    for (int i = 0; i < kWlItemFields; ++i) f2[i] = load_uniform_i32(r + kWlItemInts + i);
-    pid2 = load_uniform_i32(r + kWlItemInts + kWlPidWord + wave);
-  }
-  // The record's values are only used past the header check, so the
-  // compiler would sink their loads below it: a second round trip.  Pinning
-  // them here keeps the header and the record in one.
-#pragma unroll
-  for (int i = 0; i < kWlItemFields; ++i) asm volatile("" : "+s"(f[i]));
-  asm volatile("" : "+s"(pid));
-  if constexpr (STREAM) {
-#pragma unroll
-    for (int i = 0; i < kWlItemFields; ++i) asm volatile("" : "+s"(f2[i]));
-    asm volatile("" : "+s"(pid2));
-  }
-  if (magic != kWlMagic || key != a.wl_key) return false;
-  if constexpr (STREAM) {
-    worklist_decode(a, f, g, G, 0, 2, w);
-    worklist_decode(a, f2, g, G, 1, 2, w2);
-  } else {
-    worklist_decode(a, f, g, G, 0, 1, w);
-  }
   return true;
 }
 
 // Minimum waves per SIMD each phase-1 instantiation is compiled for (it
 // caps the registers per lane at 512 / waves).  The generic page-size mode
 // of head_dim 128 gets 2 (256 registers): its six prefetched page ids did
-// not fit 168 registers without one VGPR spilled to scratch.  The stream
-// kernel (two inlined wave loops) gets 2 as well: at 168 registers it
-// spilled 9 VGPRs to scratch, and its launches (planned, at most one
-// workgroup per CU) never run more than 2 waves per SIMD.
-constexpr int phase1_waves_per_simd(int d, int engine, int mode, bool stream) {
-  return stream ? 2 : (engine == 0 ? (d <= 128 ? (d == 128 && mode == 0 ? 2 : 3) : 1) : 1);
+// not fit 168 registers without one VGPR spilled to scratch.
+constexpr int phase1_waves_per_simd(int d, int engine, int mode) {
+  return engine == 0 ? (d <= 128 ? (d == 128 && mode == 0 ? 2 : 3) : 1) : 1;
 }
 
 // Most waves in one workgroup.  head_dim 256 takes at most 4, so that each
@@ -1599,90 +1308,143 @@ __global__ __launch_bounds__(64) void pad_plan_kernel(const Phase1Args a, int32_
   const int32_t* static_row = a.bt + (int64_t)bz * a.sbb;
   const SeqRaw raw = issue_seq_table(a, lane);
   const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)bz * a.ssl);
-  WorkItem it2{};
-  const WorkItem it1 = a.stream ? resolve_workgroup<true>(a, raw, s, h, bz, g, G, lin, static_row, static_len, lane, it2)
-                                : resolve_workgroup<false>(a, raw, s, h, bz, g, G, lin, static_row, static_len, lane, it2);
-  // Lanes 0-31 write item 1's half of the record, lanes 32-63 item 2's.
-  const bool second = lane >= kWlItemInts;
-  const int i = lane & (kWlItemInts - 1);
-  const int valid = second ? it2.valid : it1.valid;
-  const int p_begin = second ? it2.p_begin : it1.p_begin;
-  const int col_max = second ? it2.col_max : it1.col_max;
-  const int32_t* ids_row = second ? it2.ids_row : it1.ids_row;
-  const int64_t ids_stride = second ? it2.ids_stride : it1.ids_stride;
+  const WorkItem it = resolve_workgroup(a, raw, s, h, bz, g, G, lin, static_row, static_len, lane);
   int v = 0;
-  switch (i) {
-    case 0: v = second ? it2.b : it1.b; break;
-    case 1: v = second ? it2.kvh : it1.kvh; break;
-    case 2: v = p_begin; break;
-    case 3: v = second ? it2.p_end : it1.p_end; break;
-    case 4: v = second ? it2.L : it1.L; break;
-    case 5: v = second ? it2.nsplit : it1.nsplit; break;
-    case 6: v = second ? it2.slot0 : it1.slot0; break;
-    case 7: v = col_max; break;
-    case 8: v = valid; break;
-    case 9: v = a.csr ? (int)(ids_row - a.bt) : 0; break;
-    case 10: v = second ? it2.slot : it1.slot; break;
-    case 11: v = second ? it2.sstride : it1.sstride; break;
-    case 12: v = second ? it2.odd : it1.odd; break;
+  switch (lane) {
+    case 0: v = it.b; break;
+    case 1: v = it.kvh; break;
+    case 2: v = it.p_begin; break;
+    case 3: v = it.p_end; break;
+    case 4: v = it.L; break;
+    case 5: v = it.nsplit; break;
+    case 6: v = it.slot0; break;
+    case 7: v = it.col_max; break;
+    case 8: v = it.valid; break;
+    case 9: v = a.csr ? (int)(it.ids_row - a.bt) : 0; break;
     default: break;
   }
+  // A slot without an item gets an all-zero record (valid = 0), so lists
+  // planned from the same inputs are identical word for word.
+  if (!it.valid) v = 0;
   // The first page id of wave w's first block, as the decode kernel's
   // first_page_id() reads it (whole-page blocks only).
-  const int w = i - kWlPidWord;
-  if (w >= 0 && w < a.nw && valid && col_max >= 0 && a.ps % kBlockTokens == 0) {
-    const int col = min(p_begin + block_page(a, w), col_max);
-    v = ids_row[(int64_t)col * ids_stride];
+  const int w = lane - 16;
+  if (w >= 0 && w < a.nw && it.valid && it.col_max >= 0 && a.ps % kBlockTokens == 0) {
+    const int col = min(it.p_begin + block_page(a, w), it.col_max);
+    v = it.ids_row[(int64_t)col * it.ids_stride];
   }
-  // A half without an item is all zero (valid = 0), so lists planned from
-  // the same inputs are identical word for word.
-  if (!valid) v = 0;
   int32_t* r = wl + kWlHeaderInts + (int64_t)kWlRecordInts * g;
-  r[lane] = v;
+  if (lane < kWlRecordInts) r[lane] = v;
   if (g == 0 && lane < kWlHeaderInts) wl[lane] = lane == 0 ? kWlMagic : (lane == 1 ? a.wl_key : (lane == 2 ? G : 0));
 }
 
-// Where one item's results go: buffer resources over its unit's partials
-// region (slots slot0 .. slot0 + sstride * nsplit - 1, 32-bit byte offsets)
-// and its unit's output rows.
-struct ItemOut {
-  __amdgpu_buffer_rsrc_t o_rsrc, ml_rsrc;
-  _Float16* out;
-};
+// Phase 1: one workgroup per (split, kv head, sequence).
+template <int D, int MODE, int ENGINE, int GQA_T>
+__global__ __launch_bounds__(max_group_waves(D) * 64)
+    __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE, MODE))))
+void pad_phase1_kernel(const Phase1Args a) {
+#ifdef PAD_TIMELINE
+  const unsigned long long tl_entry = __builtin_amdgcn_s_memrealtime();
+  const unsigned long long tl_xcc = (unsigned long long)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15) << 32;
+#define PAD_TL_NOTE(item_slot, flags) \
+  PAD_TL_AT(lin, PAD_TL_INFO, (unsigned long long)(uint32_t)(item_slot) | tl_xcc | ((unsigned long long)(flags) << 40))
+#else
+#define PAD_TL_NOTE(item_slot, flags) \
+  do {                                \
+  } while (0)
+#endif
+  extern __shared__ float4 smem_f4[];
+  float2* sm_ml = reinterpret_cast<float2*>(smem_f4);  // [nw][16]
+  const int nw = a.nw;
+  float* sm_o = reinterpret_cast<float*>(smem_f4) + nw * 32;  // [nw][gqa][D + 4]
+  // [nw] K staging tiles (MFMA engine), after the wave states.
+  char* k_stage_all = reinterpret_cast<char*>(sm_o + nw * a.gqa * wave_row_floats<D>());
 
-template <int D>
-__device__ __forceinline__ ItemOut item_out(const Phase1Args& a, const WorkItem& it) {
-  ItemOut r;
-  const int64_t row0 = (int64_t)it.slot0 * a.gqa;
-  const uint32_t rows = (uint32_t)(it.sstride * it.nsplit * a.gqa);
-  r.o_rsrc = make_rsrc(a.o_part + row0 * D, rows * D * 4u);
-  r.ml_rsrc = make_rsrc(a.ml_part + row0, rows * 8u);
-  r.out = a.out + (int64_t)it.b * a.sob + (int64_t)(it.kvh * a.gqa) * a.soh;
-  return r;
-}
+  int s, h, bz, lin;
+  grid_pos(a, s, h, bz, lin);
+  PAD_TL_AT(blockIdx.x + a.num_splits * (blockIdx.y + a.hkv * blockIdx.z), PAD_TL_ENTRY, tl_entry);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = s + a.num_splits * (h + a.hkv * bz);
+  const int G = a.num_splits * a.hkv * a.batch;
 
-// An empty sequence's output rows: zeros (src/reference.py:32-34).
-template <int D>
-__device__ __forceinline__ void zero_rows(const Phase1Args& a, const ItemOut& io, int nw) {
-  for (int e = threadIdx.x; e < a.gqa * (D / 4); e += nw * 64) {
-    const int row = e / (D / 4);
-    *reinterpret_cast<h4_t*>(io.out + (int64_t)row * a.soh + (e - row * (D / 4)) * 4) = (h4_t)0;
+  // With a work list, the item and its first page ids arrive in one round
+  // trip.  Otherwise, with the dense table, read the first page id of this
+  // workgroup's static split before the sequence lengths arrive; it stays
+  // valid whenever the item turns out to be the static one.
+  WorkItem it;
+  int phys_first = 0;
+  bool first_known;
+  if (a.worklist != nullptr && worklist_item(a, g, G, wave, it, phys_first)) {
+    first_known = true;
+  } else {
+    // The sequence table's loads go first, then the page id and this
+    // workgroup's sequence length: one round trip for all of them.  The
+    // page-id read has no branch (a CSR index or an empty table reads a
+    // valid word that is never used), as a value loaded under a branch
+    // would be waited for where the branch joins, before the later loads.
+    const SeqRaw raw = issue_seq_table(a, lane);
+    const int32_t* static_row = a.bt + (int64_t)bz * a.sbb;
+    if constexpr (ENGINE == 0 && MODE == kModeUniform) {
+      const int col = min(s * a.pps + block_page(a, wave), a.max_pages - 1);
+      const bool use = !a.csr && a.max_pages > 0;
+      phys_first = load_uniform_i32(use ? static_row + (int64_t)col * a.sbp : (a.csr ? a.indptr : a.sl));
+    }
+    const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)bz * a.ssl);
+    it = resolve_workgroup(a, raw, s, h, bz, g, G, lin, static_row, static_len, lane);
+    first_known = !a.csr && it.b == bz && it.p_begin == s * a.pps;
   }
-}
-
-// The waves' states of one item (sm_ml / sm_o, written by the wave loops;
-// call after a barrier) merged into one fp32 state per (row, 4 columns),
-// threads over (row, 4 consecutive d).  A unit with one item is final and
-// goes to the output rows; otherwise the item's partial is stored in its
-// slot with device-scope (SC1) buffer stores, which are coherent across the
-// XCDs' L2 caches on their own, so publishing it needs no cache writeback.
-// Returns true when the item must be counted in (its unit has several).
-template <int D>
-__device__ __forceinline__ bool publish_item(const Phase1Args& a, const WorkItem& it, const ItemOut& io,
-                                             const float2* sm_ml, const float* sm_o, int nw) {
+  PAD_TL(lin, PAD_TL_ITEM);
+  if (!it.valid) {
+    PAD_TL_NOTE(-1, PAD_TL_F_NO_ITEM);
+    PAD_TL(lin, PAD_TL_EXIT);
+    return;
+  }
+  const int b = it.b;
+  const int kvh = it.kvh;
+  const int nsplit = it.nsplit;
   const int gqa = a.gqa;
-  const uint32_t my_row0 = (uint32_t)((it.slot - it.slot0) * gqa);
-  for (int e = threadIdx.x; e < gqa * (D / 4); e += nw * 64) {
+  const int total4 = gqa * (D / 4);
+  _Float16* out_bh = a.out + (int64_t)b * a.sob + (int64_t)(kvh * gqa) * a.soh;
+  if (nsplit == 0) {  // seq_len == 0: the output rows are zeros
+    for (int e = threadIdx.x; e < total4; e += nw * 64) {
+      const int row = e / (D / 4);
+      *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + (e - row * (D / 4)) * 4) = (h4_t)0;
+    }
+    PAD_TL_NOTE(g, PAD_TL_F_SINGLE);
+    PAD_TL(lin, PAD_TL_EXIT);
+    return;
+  }
+  if constexpr (ENGINE == 0 && MODE == kModeUniform) {
+    if (!first_known) phys_first = first_page_id(a, it.ids_row, it.ids_stride, it.col_max, it.p_begin, wave);
+  }
+  const int t_begin = it.p_begin * a.ps;
+  const int t_end = min(it.p_end * a.ps, it.L);
+  const int nblk = (t_end - t_begin + kBlockTokens - 1) / kBlockTokens;
+
+  if constexpr (ENGINE == 0) {
+    wave_loop_mfma<D, MODE>(a, phys_first, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw,
+                               lane, sm_ml, sm_o, k_stage_all + wave * k_stage_bytes<D>(),
+                               k_stage_all + nw * k_stage_bytes<D>());
+  } else {
+    wave_loop_valu<D, MODE == kModeUniform, GQA_T>(a, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw, lane,
+                                      sm_ml, sm_o);
+  }
+  __syncthreads();
+  PAD_TL(lin, PAD_TL_LOOP_END);
+
+  // Merge the waves' states: threads over (row, 4 consecutive d).  With a
+  // single split the result is final; otherwise it is this split's partial.
+  // Partials are stored and later loaded with device-scope (SC1) buffer
+  // accesses, which are coherent across the XCDs' L2 caches on their own, so
+  // publishing a partial needs no cache writeback.  The items of a (sequence,
+  // kv head) own consecutive slots, addressed with 32-bit byte offsets.
+  const int64_t seq_row0 = (int64_t)it.slot0 * gqa;
+  const uint32_t region_rows = (uint32_t)(nsplit * gqa);
+  const __amdgpu_buffer_rsrc_t o_rsrc = make_rsrc(a.o_part + seq_row0 * D, region_rows * D * 4u);
+  const __amdgpu_buffer_rsrc_t ml_rsrc = make_rsrc(a.ml_part + seq_row0, region_rows * 8u);
+  const int my_split = g - it.slot0;
+  for (int e = threadIdx.x; e < total4; e += nw * 64) {
     const int row = e / (D / 4);
     const int col = (e - row * (D / 4)) * 4;
     // Unrolled over the largest wave count, so all LDS reads issue together.
@@ -1709,300 +1471,102 @@ __device__ __forceinline__ bool publish_item(const Phase1Args& a, const WorkItem
         acc += c * ow[w];
       }
     }
-    if (it.nsplit == 1) {
+    if (nsplit == 1) {
       const float inv = 1.f / Ls;  // Ls >= 1: the max token contributes 2^0
       h4_t hv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
-      *reinterpret_cast<h4_t*>(io.out + (int64_t)row * a.soh + col) = hv;
+      *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + col) = hv;
     } else {
-      const uint32_t r = my_row0 + (uint32_t)row;
-      store_device(io.o_rsrc, (r * D + col) * 4u, acc);
-      if (col == 0) store_device(io.ml_rsrc, r * 8u, make_float2(M, Ls));
+      const uint32_t r = (uint32_t)(my_split * gqa + row);
+      store_device(o_rsrc, (r * D + col) * 4u, acc);
+      if (col == 0) store_device(ml_rsrc, r * 8u, make_float2(M, Ls));
     }
   }
-  return it.nsplit > 1;
-}
-
-// First level of a two-level merge (units with more than kTwoLevelSplits
-// items; one workgroup reading every partial was the tail: 256 splits of 8
-// rows are 1 MB, ~17 us).  The last arrival of each group of 16 consecutive
-// items folds the group into the slot of the group's first item (nothing
-// else reads those slots any more), publishes it like a partial and returns
-// true; the other arrivals return false.  stride / count become the second
-// level's (entry e' = item 16 e').  Whole workgroup; call with the item's
-// partial stores complete and after a barrier.
-template <int D>
-__device__ __forceinline__ bool merge_group(const Phase1Args& a, const WorkItem& it, const ItemOut& io, float2* sm_ml,
-                                            int nw, int* flag, int& stride, int& count) {
-  const int gqa = a.gqa;
-  const int entry = (it.slot - it.slot0) >> (it.sstride - 1);  // sstride 1 or 2; entry 0 may sit at +odd
-  const int grp0 = entry & ~15;
-  const int gsize = min(16, it.nsplit - grp0);
-  const int grp_slot = grp0 * it.sstride + (grp0 == 0 ? it.odd : 0);  // relative to slot0
-  int* group_counter = a.counters + (int64_t)a.batch * a.hkv + it.slot0 + grp_slot;
-  if (threadIdx.x == 0) *flag = (atomicAdd(group_counter, 1) == gsize - 1);
-  __syncthreads();
-  if (!*flag) return false;
-  // Each element's O is read and then overwritten by its own thread, but a
-  // row's (m, l) is read by every thread of the row, and a row can span
-  // waves and loop passes (head_dim 96: 24 elements per row): the group's
-  // (m, l) goes to LDS first and to the slot only after a barrier.
-  for (int e = threadIdx.x; e < gqa * (D / 4); e += nw * 64) {
-    const int row = e / (D / 4);
-    const int col = (e - row * (D / 4)) * 4;
-    float m = kNegInf, l = 0.f;
-    f4_t acc = (f4_t)0.f;
-    merge_partials(io.o_rsrc, io.ml_rsrc, grp0, gsize, it.sstride, it.odd, gqa, row, col, D, m, l, acc);
-    const uint32_t r = (uint32_t)(grp_slot * gqa + row);
-    store_device(io.o_rsrc, (r * D + col) * 4u, acc);
-    if (col == 0) sm_ml[row] = make_float2(m, l);
-  }
-  __syncthreads();
-  if (threadIdx.x < gqa) store_device(io.ml_rsrc, (uint32_t)(grp_slot * gqa + threadIdx.x) * 8u, sm_ml[threadIdx.x]);
-  if (threadIdx.x == 0) atomicExch(group_counter, 0);
-  stride = 16 * it.sstride;
-  count = (it.nsplit + 15) >> 4;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  return true;
-}
-
-// The last arrival of a unit folds its `count` entries (entry e in slot
-// e * stride of the region, entry 0 at +odd) into the fp16 output rows and
-// resets the unit's counter for the next launch.
-template <int D>
-__device__ __forceinline__ void merge_unit(const Phase1Args& a, const WorkItem& it, const ItemOut& io, int stride,
-                                           int count, int nw) {
-  const int gqa = a.gqa;
-  for (int e = threadIdx.x; e < gqa * (D / 4); e += nw * 64) {
-    const int row = e / (D / 4);
-    const int col = (e - row * (D / 4)) * 4;
-    float m = kNegInf, l = 0.f;
-    f4_t acc = (f4_t)0.f;
-    merge_partials(io.o_rsrc, io.ml_rsrc, 0, count, stride, it.odd, gqa, row, col, D, m, l, acc);
-    const float inv = 1.f / l;
-    h4_t hv;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
-    *reinterpret_cast<h4_t*>(io.out + (int64_t)row * a.soh + col) = hv;
-  }
-  if (threadIdx.x == 0) atomicExch(a.counters + (int64_t)it.b * a.hkv + it.kvh, 0);
-}
-
-// Phase 1 with the split merge fused in: one workgroup per (split, kv head,
-// sequence) slot of the grid, which processes one work item, or with STREAM
-// (the stream kernel of planned launches) up to two: the two stream items
-// of its range, each wave streaming item 1's blocks and then item 2's.
-template <int D, int MODE, int ENGINE, int GQA_T, bool STREAM>
-__global__ __launch_bounds__(max_group_waves(D) * 64)
-    __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE, MODE, STREAM))))
-void pad_phase1_kernel(const Phase1Args a) {
-#ifdef PAD_TIMELINE
-  const unsigned long long tl_entry = __builtin_amdgcn_s_memrealtime();
-  const unsigned long long tl_xcc = (unsigned long long)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15) << 32;
-#define PAD_TL_NOTE(item_slot, flags) \
-  PAD_TL_AT(lin, PAD_TL_INFO, (unsigned long long)(uint32_t)(item_slot) | tl_xcc | ((unsigned long long)(flags) << 40))
-#else
-#define PAD_TL_NOTE(item_slot, flags) \
-  do {                                \
-  } while (0)
-#endif
-  extern __shared__ float4 smem_f4[];
-  float2* sm_ml = reinterpret_cast<float2*>(smem_f4);  // [nw][16]
-  const int nw = a.nw;
-  float* sm_o = reinterpret_cast<float*>(smem_f4) + nw * 32;  // [nw][gqa][D + 4]
-  // [nw] K staging tiles (MFMA engine), after the wave states.
-  char* k_stage_all = reinterpret_cast<char*>(sm_o + nw * a.gqa * wave_row_floats<D>());
-  // STREAM: item 2's wave states, after the staging tiles (and Q^T copy).
-  float2* sm_ml2 =
-      reinterpret_cast<float2*>(k_stage_all + nw * k_stage_bytes<D>() + (q_in_lds<D>() ? k_stage_bytes<D>() : 0));
-  float* sm_o2 = reinterpret_cast<float*>(sm_ml2 + nw * 16);
-
-  int s, h, bz, lin;
-  grid_pos(a, s, h, bz, lin);
-  PAD_TL_AT(blockIdx.x + a.num_splits * (blockIdx.y + a.hkv * blockIdx.z), PAD_TL_ENTRY, tl_entry);
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = s + a.num_splits * (h + a.hkv * bz);
-  const int G = a.num_splits * a.hkv * a.batch;
-
-  // With a work list, the items and their first page ids arrive in one
-  // round trip.  Otherwise, with the dense table, read the first page id of
-  // this workgroup's static split before the sequence lengths arrive; it
-  // stays valid whenever the item turns out to be the static one.
-  WorkItem it, it2{};
-  int phys_first = 0, phys2 = 0;
-  bool first_known, from_list = false;
-  if (a.worklist != nullptr && worklist_item<STREAM>(a, g, G, wave, it, phys_first, it2, phys2)) {
-    first_known = from_list = true;
-  } else {
-    // The sequence table's loads go first, then the page id and this
-    // workgroup's sequence length: one round trip for all of them.  The
-    // page-id read has no branch (a CSR index or an empty table reads a
-    // valid word that is never used), as a value loaded under a branch
-    // would be waited for where the branch joins, before the later loads.
-    const SeqRaw raw = issue_seq_table(a, lane);
-    const int32_t* static_row = a.bt + (int64_t)bz * a.sbb;
-    if constexpr (ENGINE == 0 && MODE == kModeUniform) {
-      const int col = min(s * a.pps + block_page(a, wave), a.max_pages - 1);
-      const bool use = !a.csr && a.max_pages > 0;
-      phys_first = load_uniform_i32(use ? static_row + (int64_t)col * a.sbp : (a.csr ? a.indptr : a.sl));
-    }
-    const int static_len = load_uniform_i32(a.csr ? a.indptr : a.sl + (int64_t)bz * a.ssl);
-    it = resolve_workgroup<STREAM>(a, raw, s, h, bz, g, G, lin, static_row, static_len, lane, it2);
-    first_known = !a.csr && it.b == bz && it.p_begin == s * a.pps;
-  }
-  if constexpr (!STREAM) {  // per-unit items only: consecutive slots (lets the merge fold these constants)
-    it.sstride = 1;
-    it.odd = 0;
-  }
-  PAD_TL(lin, PAD_TL_ITEM);
-  if (!it.valid && !(STREAM && it2.valid)) {
-    PAD_TL_NOTE(-1, PAD_TL_F_NO_ITEM);
-    PAD_TL(lin, PAD_TL_EXIT);
-    return;
-  }
-  if constexpr (!STREAM) {
-    if (it.nsplit == 0) {  // seq_len == 0: the output rows are zeros
-      zero_rows<D>(a, item_out<D>(a, it), nw);
-      PAD_TL_NOTE(g, PAD_TL_F_SINGLE);
-      PAD_TL(lin, PAD_TL_EXIT);
-      return;
-    }
-  }
-  if constexpr (ENGINE == 0 && MODE == kModeUniform) {
-    if (!first_known && (!STREAM || it.valid))
-      phys_first = first_page_id(a, it.ids_row, it.ids_stride, it.col_max, it.p_begin, wave);
-    if (STREAM && !from_list && it2.valid)
-      phys2 = first_page_id(a, it2.ids_row, it2.ids_stride, it2.col_max, it2.p_begin, wave);
-  }
-
-  // Each wave streams its blocks of the item(s) into its LDS state.
-  auto stream_item = [&](const WorkItem& w, int pid, float2* ml, float* o) {
-    const int t_begin = w.p_begin * a.ps;
-    const int t_end = min(w.p_end * a.ps, w.L);
-    const int nblk = (t_end - t_begin + kBlockTokens - 1) / kBlockTokens;
-    if constexpr (ENGINE == 0) {
-      wave_loop_mfma<D, MODE>(a, pid, w.ids_row, w.ids_stride, w.b, w.kvh, t_begin, t_end, nblk, wave, nw, lane, ml,
-                              o, k_stage_all + wave * k_stage_bytes<D>(), k_stage_all + nw * k_stage_bytes<D>());
-    } else {
-      wave_loop_valu<D, MODE == kModeUniform, GQA_T>(a, w.ids_row, w.ids_stride, w.b, w.kvh, t_begin, t_end, nblk,
-                                                     wave, nw, lane, ml, o);
-    }
-  };
-  if constexpr (STREAM) {
-    static_assert(ENGINE == 0 && MODE == kModeUniform, "stream kernel: MFMA engine, whole-page blocks");
-    // Item 1, whose loop issues each wave's first tile of item 2 ahead;
-    // without item 1 pages the same call (no blocks) only issues those.
-    const bool run1 = it.valid && it.nsplit > 0;
-    const bool run2 = it2.valid && it2.nsplit > 0;
-    NextItem nx;
-    nx.ids_row = it2.ids_row;
-    nx.ids_stride = it2.ids_stride;
-    nx.b = it2.b;
-    nx.kvh = it2.kvh;
-    nx.t_begin = it2.p_begin * a.ps;
-    nx.nblk = run2 ? (min(it2.p_end * a.ps, it2.L) - nx.t_begin + kBlockTokens - 1) / kBlockTokens : 0;
-    nx.phys_first = phys2;
-    TileAhead<D> ah;
-    char* k_stage = k_stage_all + wave * k_stage_bytes<D>();
-    const int t_begin = run1 ? it.p_begin * a.ps : 0;
-    const int t_end = run1 ? min(it.p_end * a.ps, it.L) : 0;
-    wave_loop_mfma<D, MODE, false, true>(a, phys_first, it.ids_row, it.ids_stride, it.b, it.kvh, t_begin, t_end,
-                                         (t_end - t_begin + kBlockTokens - 1) / kBlockTokens, wave, nw, lane, sm_ml,
-                                         sm_o, k_stage, nullptr, &ah, &nx);
-    if (run2)
-      wave_loop_mfma<D, MODE, true, false>(a, phys2, it2.ids_row, it2.ids_stride, it2.b, it2.kvh, nx.t_begin,
-                                           min(it2.p_end * a.ps, it2.L), nx.nblk, wave, nw, lane, sm_ml2, sm_o2,
-                                           k_stage, nullptr, &ah, nullptr);
-  } else {
-    stream_item(it, phys_first, sm_ml, sm_o);
-  }
-  __syncthreads();
-  PAD_TL(lin, PAD_TL_LOOP_END);
-
-  // Merge the waves' states: the output rows of a unit with one item, else
-  // the item's partial.
-  bool need1 = false, need2 = false;
-  const ItemOut io = item_out<D>(a, it);
-  const ItemOut io2 = item_out<D>(a, it2);
-  if constexpr (STREAM) {
-    if (it.valid) {
-      if (it.nsplit == 0)
-        zero_rows<D>(a, io, nw);
-      else
-        need1 = publish_item<D>(a, it, io, sm_ml, sm_o, nw);
-    }
-    if (it2.valid) {
-      if (it2.nsplit == 0)
-        zero_rows<D>(a, io2, nw);
-      else
-        need2 = publish_item<D>(a, it2, io2, sm_ml2, sm_o2, nw);
-    }
-  } else {
-    need1 = publish_item<D>(a, it, io, sm_ml, sm_o, nw);
-  }
-  if (!need1 && !need2) {
+  if (nsplit == 1) {
     PAD_TL(lin, PAD_TL_PUBLISHED);
-    PAD_TL_NOTE(g, PAD_TL_F_SINGLE | ((STREAM && it.valid && it2.valid) ? PAD_TL_F_TWO : 0));
+    PAD_TL_NOTE(g, PAD_TL_F_SINGLE);
     PAD_TL(lin, PAD_TL_EXIT);
     return;
   }
 
-  // Split-K merge, fused: the last workgroup of a (sequence, kv head) unit
-  // to arrive folds every item's partial into the output.  A workgroup
-  // counts itself in only after its partial stores have completed at device
-  // scope (vmcnt(0) covers stores on this architecture); the last one to
-  // arrive reads the partials with device-scope loads and resets the
-  // counter to zero for the next launch.  Units with more than
-  // kTwoLevelSplits items merge in two levels (merge_group).
-  __shared__ int s_flag[4];
+  // Split-K merge, fused: the last workgroup of this (sequence, kv head) to
+  // arrive folds every split's partial into the output.  A workgroup counts
+  // itself in only after its partial stores have completed at device scope
+  // (vmcnt(0) covers stores on this architecture); the last one to arrive
+  // reads the partials with device-scope loads and resets the counter to
+  // zero for the next launch.
+  //
+  // Past kTwoLevelSplits splits one workgroup reading every partial is the
+  // tail (256 splits of 8 rows: 1 MB, ~17 us), so the merge takes two
+  // levels: the last arrival of each group of 16 consecutive splits folds
+  // the group into the slot of its first split (nothing else reads those
+  // slots any more), publishes it like a partial and counts the group in;
+  // the last group folds the group results.
+  __shared__ int s_last;
+  int* unit_counter = a.counters + (int64_t)b * a.hkv + kvh;
+  int stride = 1, count = nsplit;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   PAD_TL(lin, PAD_TL_PUBLISHED);
-  int tl_flags = (STREAM && it.valid && it2.valid) ? PAD_TL_F_TWO : 0;
+  int tl_flags = 0;
   (void)tl_flags;
-  int stride1 = it.sstride, count1 = it.nsplit;
-  int stride2 = it2.sstride, count2 = it2.nsplit;
-  if (need1 && it.nsplit > kTwoLevelSplits) {
-    need1 = merge_group<D>(a, it, io, sm_ml, nw, &s_flag[2], stride1, count1);
-    tl_flags |= PAD_TL_F_GROUP;
-  }
-  if constexpr (STREAM) {
-    if (need2 && it2.nsplit > kTwoLevelSplits) need2 = merge_group<D>(a, it2, io2, sm_ml, nw, &s_flag[3], stride2, count2);
-  }
-  if (!need1 && !need2) {
-    PAD_TL(lin, PAD_TL_ARRIVED);
-    PAD_TL_NOTE(g, tl_flags & PAD_TL_F_TWO);
-    PAD_TL(lin, PAD_TL_EXIT);
-    return;
-  }
-  if constexpr (STREAM) {
-    // Both units' arrivals in one atomic instruction (lanes 0 and 1).
-    if (threadIdx.x < 2) {
-      const bool second = threadIdx.x == 1;
-      const bool need = second ? need2 : need1;
-      int* counter = a.counters + (second ? (int64_t)it2.b * a.hkv + it2.kvh : (int64_t)it.b * a.hkv + it.kvh);
-      const int count = second ? count2 : count1;
-      s_flag[threadIdx.x] = need && atomicAdd(counter, 1) == count - 1;
+  if (nsplit > kTwoLevelSplits) {
+    const int grp0 = my_split & ~15;  // first split of this group
+    const int gsize = min(16, nsplit - grp0);
+    int* group_counter = a.counters + (int64_t)a.batch * a.hkv + it.slot0 + grp0;
+    if (threadIdx.x == 0) s_last = (atomicAdd(group_counter, 1) == gsize - 1);
+    __syncthreads();
+    if (!s_last) {
+      PAD_TL(lin, PAD_TL_ARRIVED);
+      PAD_TL_NOTE(g, 0);
+      PAD_TL(lin, PAD_TL_EXIT);
+      return;
     }
-  } else {
-    if (threadIdx.x == 0) s_flag[0] = need1 && atomicAdd(a.counters + (int64_t)it.b * a.hkv + it.kvh, 1) == count1 - 1;
+    tl_flags = PAD_TL_F_GROUP;
+    // Each element's O is read and then overwritten by its own thread, but
+    // a row's (m, l) is read by every thread of the row, and a row can span
+    // waves and loop passes (head_dim 96: 24 elements per row): the group's
+    // (m, l) goes to LDS first and to the slot only after a barrier.
+    for (int e = threadIdx.x; e < total4; e += nw * 64) {
+      const int row = e / (D / 4);
+      const int col = (e - row * (D / 4)) * 4;
+      float m = kNegInf, l = 0.f;
+      f4_t acc = (f4_t)0.f;
+      merge_partials(o_rsrc, ml_rsrc, grp0, gsize, 1, gqa, row, col, D, m, l, acc);
+      const uint32_t r = (uint32_t)(grp0 * gqa + row);
+      store_device(o_rsrc, (r * D + col) * 4u, acc);
+      if (col == 0) sm_ml[row] = make_float2(m, l);
+    }
+    __syncthreads();
+    if (threadIdx.x < gqa) store_device(ml_rsrc, (uint32_t)(grp0 * gqa + threadIdx.x) * 8u, sm_ml[threadIdx.x]);
+    if (threadIdx.x == 0) atomicExch(group_counter, 0);
+    stride = 16;
+    count = (nsplit + 15) >> 4;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
   }
+  if (threadIdx.x == 0) s_last = (atomicAdd(unit_counter, 1) == count - 1);
   __syncthreads();
   PAD_TL(lin, PAD_TL_ARRIVED);
-  const bool last1 = s_flag[0] != 0;
-  const bool last2 = STREAM && s_flag[1] != 0;
-  if (!last1 && !last2) {
+  if (!s_last) {
     PAD_TL_NOTE(g, tl_flags);
     PAD_TL(lin, PAD_TL_EXIT);
     return;
   }
-  if (last1) merge_unit<D>(a, it, io, stride1, count1, nw);
-  if constexpr (STREAM) {
-    if (last2) merge_unit<D>(a, it2, io2, stride2, count2, nw);
+  for (int e = threadIdx.x; e < total4; e += nw * 64) {
+    const int row = e / (D / 4);
+    const int col = (e - row * (D / 4)) * 4;
+    float m = kNegInf, l = 0.f;
+    f4_t acc = (f4_t)0.f;
+    merge_partials(o_rsrc, ml_rsrc, 0, count, stride, gqa, row, col, D, m, l, acc);
+    const float inv = 1.f / l;
+    h4_t hv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
+    *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + col) = hv;
   }
+  if (threadIdx.x == 0) atomicExch(unit_counter, 0);
   PAD_TL(lin, PAD_TL_MERGED);
   PAD_TL_NOTE(g, tl_flags | PAD_TL_F_MERGER);
   PAD_TL(lin, PAD_TL_EXIT);
@@ -2104,25 +1668,6 @@ static bool latency_bound_shape(const pad_decode_dims* d, int num_cus, bool csr)
   return units * blocks_per_seq <= 16 * (int64_t)num_cus;
 }
 
-// LDS of a stream workgroup's second set of wave states (item 2's).
-static size_t stream_lds_bytes(int nw, int gqa, int d) {
-  return (size_t)nw * (16 * sizeof(float2) + (size_t)gqa * (d + 4) * sizeof(float));
-}
-
-// Launches that run the stream kernel: those the in-kernel planner plans
-// (heuristic split count, at least 2 splits, batch <= kPlanMaxBatch, not an
-// oversubscribed grid), with whole-page 16-token blocks, the MFMA engine,
-// head_dim 64 or 128, and LDS for two sets of wave states.  Their workgroups
-// get stream items when the lengths are ragged (two workspace slots each).
-static bool stream_shape(const pad_decode_dims* d, int num_splits, int num_cus, int engine, int S, int nw,
-                         bool latency_bound) {
-  if (num_splits != 0 || S < 2 || engine != 0 || d->batch > kPlanMaxBatch || d->max_pages >= (1 << 23)) return false;
-  if (oversubscribed_shape(d, num_splits, num_cus, latency_bound)) return false;
-  if (d->page_size % kBlockTokens != 0 || (d->head_dim != 64 && d->head_dim != 128)) return false;
-  const int gqa = d->num_q_heads / d->num_kv_heads;
-  return group_lds_bytes(nw, gqa, d->head_dim, engine) + stream_lds_bytes(nw, gqa, d->head_dim) <= (size_t)kLdsBudget;
-}
-
 static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int engine, bool csr,
                      pad_decode_plan_t* p) {
   const int st = validate_dims(d);
@@ -2202,21 +1747,13 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   p->waves_per_group = nw;
   p->single_pass = (S == 1) ? 1 : 0;
   p->engine = engine;
-  p->slots_per_group = stream_shape(d, num_splits, num_cus, engine, S, nw, latency_bound) ? 2 : 1;
-  if (csr && p->slots_per_group == 2) {
-    // Never more slots than the dense plan of the same dims (see above).
-    pad_decode_plan_t dense;
-    plan_impl(d, 0, num_cus, engine, false, &dense);
-    if (2 * S > dense.num_splits * dense.slots_per_group) p->slots_per_group = 1;
-  }
+  p->reserved = 0;
   p->counters = 0;
-  p->workspace_bytes =
-      p->single_pass ? 0 : workspace_layout(d, S * p->slots_per_group, nullptr, nullptr, nullptr);
+  p->workspace_bytes = p->single_pass ? 0 : workspace_layout(d, S, nullptr, nullptr, nullptr);
   // One arrival counter per unit and, where a unit may get more than
-  // kTwoLevelSplits items, one per workspace slot for the merge's groups.
+  // kTwoLevelSplits items, one per item slot for the merge's groups.
   const int64_t units64 = (int64_t)d->batch * d->num_kv_heads;
-  p->counters = p->single_pass ? 0
-                               : units64 + (units64 * S > kTwoLevelSplits ? units64 * S * p->slots_per_group : 0);
+  p->counters = p->single_pass ? 0 : units64 + (units64 * S > kTwoLevelSplits ? units64 * S : 0);
   return PAD_OK;
 }
 
@@ -2236,9 +1773,9 @@ static int device_cus(int* out) {
   return PAD_OK;
 }
 
-template <int D, int MODE, int ENGINE, int GQA_T, bool STREAM = false>
+template <int D, int MODE, int ENGINE, int GQA_T>
 static hipError_t launch_p1(const Phase1Args& a, dim3 grid, int nw, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((pad_phase1_kernel<D, MODE, ENGINE, GQA_T, STREAM>), grid, dim3(nw * 64), lds, st, a);
+  hipLaunchKernelGGL((pad_phase1_kernel<D, MODE, ENGINE, GQA_T>), grid, dim3(nw * 64), lds, st, a);
   return hipGetLastError();
 }
 
@@ -2263,9 +1800,6 @@ static hipError_t dispatch_engine(const Phase1Args& a, dim3 grid, int nw, size_t
 template <int D>
 static hipError_t dispatch_phase1(const Phase1Args& a, dim3 grid, int nw, size_t lds, int engine,
                                   hipStream_t st) {
-  if constexpr (D == 64 || D == 128) {
-    if (a.stream) return launch_p1<D, kModeUniform, 0, 0, true>(a, grid, nw, lds, st);
-  }
   if (a.ps % kBlockTokens == 0) return dispatch_engine<D, kModeUniform>(a, grid, nw, lds, engine, st);
   if (engine == 0) {
     switch (a.ps) {
@@ -2295,7 +1829,7 @@ struct Launch {
 // decide the grid and which item each workgroup gets (FNV-1a).
 static int plan_key(const Phase1Args& a) {
   const int f[] = {a.batch, a.hkv, a.max_pages, a.num_splits, a.nw, a.csr, a.balance,
-                   a.ps, a.pps, a.gqa, a.pair_heads, a.min_chunk, a.stream};
+                   a.ps, a.pps, a.gqa, a.pair_heads, a.min_chunk};
   uint32_t h = 2166136261u;
   for (int x : f) {
     h ^= (uint32_t)x;
@@ -2346,7 +1880,7 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   const int S = plan.num_splits;
   float* o_part = nullptr;
   float2* ml_part = nullptr;
-  if (io && !plan.single_pass) workspace_layout(d, S * plan.slots_per_group, ws, &o_part, &ml_part);
+  if (io && !plan.single_pass) workspace_layout(d, S, ws, &o_part, &ml_part);
 
   Phase1Args& a = L->a;
   a.q = static_cast<const _Float16*>(q);
@@ -2389,9 +1923,6 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   if (num_splits == 0 && !plan.single_pass && d->batch <= kPlanMaxBatch && d->max_pages < (1 << 23))
     a.balance = oversubscribed_shape(d, num_splits, cus, latency_bound_shape(d, cus, csr)) ? 2 : 1;
   a.min_chunk = ceil_div(kMinBlocks * kBlockTokens, d->page_size);
-  // Stream items only where the in-kernel planner runs (plan_impl checks
-  // the rest of the conditions).
-  a.stream = (plan.slots_per_group == 2 && a.balance == 1) ? 1 : 0;
   a.pair_heads = ((d->head_dim * 2) % 128 != 0 && d->num_kv_heads % 2 == 0 &&
                   ((int64_t)S * d->num_kv_heads * d->batch) % 16 == 0) ? 1 : 0;
   a.ps_shift = -1;
@@ -2404,7 +1935,7 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   a.tl_launch = 0;
 #endif
   L->nw = plan.waves_per_group;
-  L->lds = group_lds_bytes(L->nw, gqa, d->head_dim, engine) + (a.stream ? stream_lds_bytes(L->nw, gqa, d->head_dim) : 0);
+  L->lds = group_lds_bytes(L->nw, gqa, d->head_dim, engine);
   L->grid = dim3(S, d->num_kv_heads, d->batch);
   return PAD_OK;
 }

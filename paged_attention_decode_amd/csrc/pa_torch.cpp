@@ -452,7 +452,6 @@ py::dict plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t 
   r["single_pass"] = p.single_pass;
   r["workspace_bytes"] = p.workspace_bytes;
   r["counters"] = p.counters;
-  r["slots_per_group"] = p.slots_per_group;
   return r;
 }
 

@@ -18,13 +18,6 @@ at least one (sequence, kv head) unit per CU and batch <= 256 get a grid of
 OVERSUBSCRIBE_SPLITS items per unit, which the kernel fills from the
 lengths: one item per unit when every sequence is full, equal page chunks
 otherwise.
-
-Planned launches of whole-page blocks at head_dim 64 or 128 run the stream
-kernel (``slots_per_group`` 2): on ragged lengths its workgroups take equal
-page ranges of the units laid end to end, each range holding at most two
-units' pages.  :func:`stream_items` restates that in-kernel plan
-(``plan_stream`` in csrc/pa_decode.hip) so tests can compare the planner
-kernel's work lists with it.
 """
 
 from __future__ import annotations
@@ -40,8 +33,6 @@ LDS_BUDGET = 136 * 1024    # LDS of one workgroup: wave merge + MFMA staging
 OVERSUBSCRIBE_SPLITS = 4   # items per unit on an oversubscribed grid
 PLAN_MAX_BATCH = 256       # largest batch the in-kernel planner handles
 TWO_LEVEL_SPLITS = 48      # units with more splits merge in two levels (groups of 16)
-PLAN_MAX_PAGES = 1 << 23   # the planner's page counts stay below this
-STREAM_MAX_UNIT_PAGES = 1 << 28  # stream items: at most this many unit pages, else per-unit chunks
 
 
 @dataclass(frozen=True)
@@ -52,7 +43,6 @@ class Plan:
     single_pass: bool
     workspace_bytes: int
     counters: int
-    slots_per_group: int = 1
 
 
 def _cdiv(a: int, b: int) -> int:
@@ -65,23 +55,6 @@ def group_lds_bytes(nw: int, gqa: int, head_dim: int, engine: int = 0) -> int:
     stage = 16 * (2 * head_dim + 16) if engine == 0 else 0
     q_stage = stage if engine == 0 and head_dim >= 256 else 0
     return nw * (16 * 8 + gqa * (head_dim + 4) * 4 + stage) + q_stage
-
-
-def stream_lds_bytes(nw: int, gqa: int, head_dim: int) -> int:
-    """LDS of a stream workgroup's second set of wave states."""
-    return nw * (16 * 8 + gqa * (head_dim + 4) * 4)
-
-
-def stream_shape(batch: int, gqa: int, num_kv_heads: int, head_dim: int, page_size: int, max_pages: int,
-                 num_splits: int, num_cus: int, engine: int, s: int, nw: int, latency_bound: bool) -> bool:
-    """Launches that run the stream kernel (two workspace slots per workgroup)."""
-    if num_splits != 0 or s < 2 or engine != 0 or batch > PLAN_MAX_BATCH or max_pages >= PLAN_MAX_PAGES:
-        return False
-    if oversubscribed(batch, num_kv_heads, max_pages, latency_bound, num_cus):
-        return False
-    if page_size % BLOCK_TOKENS or head_dim not in (64, 128):
-        return False
-    return group_lds_bytes(nw, gqa, head_dim, engine) + stream_lds_bytes(nw, gqa, head_dim) <= LDS_BUDGET
 
 
 def pages_per_seq(batch: int, max_pages: int, csr: bool) -> int:
@@ -133,16 +106,10 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     cap_w = max(min((LDS_BUDGET - fixed) // per_wave, 4 if head_dim >= 256 else MAX_WAVES), 1)
     nw = max(min(nw, cap_w), 1)
     single = s == 1
-    spg = 2 if stream_shape(batch, gqa, num_kv_heads, head_dim, page_size, max_pages, num_splits, num_cus, engine,
-                            s, nw, latency_bound) else 1
-    if csr and spg == 2:  # never more slots than the dense plan of the same dims
-        dense = plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, max_pages, 0, num_cus, engine)
-        if 2 * s > dense.num_splits * dense.slots_per_group:
-            spg = 1
-    ws = 0 if single else workspace_bytes(batch, num_kv_heads, gqa, head_dim, s * spg)
+    ws = 0 if single else workspace_bytes(batch, num_kv_heads, gqa, head_dim, s)
     units = batch * num_kv_heads
-    counters = 0 if single else units + (units * s * spg if units * s > TWO_LEVEL_SPLITS else 0)
-    return Plan(s, pps, nw, single, ws, counters, spg)
+    counters = 0 if single else units + (units * s if units * s > TWO_LEVEL_SPLITS else 0)
+    return Plan(s, pps, nw, single, ws, counters)
 
 
 def oversubscribed(batch: int, num_kv_heads: int, max_pages: int, latency_bound: bool, num_cus: int) -> bool:
@@ -155,94 +122,3 @@ def workspace_bytes(batch: int, num_kv_heads: int, gqa: int, head_dim: int, num_
     """256 B alignment slack + fp32 O [B, Hkv, S, gqa, D] + (m, l) [B, Hkv, S, gqa]."""
     rows = batch * num_kv_heads * num_splits * gqa
     return 256 + rows * head_dim * 4 + rows * 8
-
-
-@dataclass(frozen=True)
-class StreamItem:
-    """One stream item: pages [p_begin, p_end) of unit (b, kvh); its partial in slot ``slot``; the unit's
-    ``nsplit`` items in slots slot0 + 2 e (+ ``odd`` for e = 0); nsplit 0 = the unit's zero rows."""
-    b: int
-    kvh: int
-    p_begin: int
-    p_end: int
-    nsplit: int
-    slot0: int
-    odd: int
-    slot: int
-
-
-def stream_span(pages: list[int], num_kv_heads: int, grid: int, min_chunk: int):
-    """(T, W) of the stream plan: each unit counts as max(pages, T) virtual pages, W in all; None when the
-    kernel uses per-unit chunks instead (ranges shorter than min_chunk pages, or too many pages)."""
-    hkv, units = num_kv_heads, len(pages) * num_kv_heads
-    up = sum(pages) * hkv
-    if up < grid * min_chunk or up > STREAM_MAX_UNIT_PAGES:
-        return None
-
-    def w_of(t):
-        return hkv * sum(max(p, t) for p in pages)
-
-    t = _cdiv(up, grid)
-    w = w_of(t)
-    if w > grid * t:
-        t1 = _cdiv(w, grid)
-        w1 = w_of(t1)
-        if w1 <= grid * t1:
-            t, w = t1, w1
-        else:
-            t = _cdiv(up, grid - units)
-            w = w_of(t)
-    return t, w
-
-
-def stream_items(pages: list[int], num_kv_heads: int, grid: int, min_chunk: int):
-    """The stream items of every workgroup of a planned launch, or None when the kernel uses per-unit chunks.
-
-    Restates ``plan_stream`` (csrc/pa_decode.hip) in exact integer arithmetic: ``pages[b]`` = pages in use
-    by sequence b, ``grid`` = G workgroups, ``min_chunk`` = fewest pages per item.  Returns a list of G
-    pairs (item 1, item 2), each a StreamItem or None."""
-    hkv, units = num_kv_heads, len(pages) * num_kv_heads
-    span = stream_span(pages, hkv, grid, min_chunk)
-    if span is None:
-        return None
-    t, w = span
-    starts, pos = [], 0  # virtual start of unit (b, h), in (b, h) order
-    for p in pages:
-        v = max(p, t)
-        for _ in range(hkv):
-            starts.append(pos)
-            pos += v
-    assert pos == w
-
-    def range_of(x):
-        return ((x + 1) * grid - 1) // w
-
-    def range_lo(r):
-        return r * w // grid
-
-    def item(u, lo, hi, slot):
-        b, h = divmod(u, hkv)
-        su, p = starts[u], pages[b]
-        if p == 0:
-            return StreamItem(b, h, 0, 0, 0, slot, 0, slot)
-        gf = range_of(su)
-        return StreamItem(b, h, lo - su, min(hi - su, p), range_of(su + p - 1) - gf + 1, 2 * gf,
-                          int(range_lo(gf) != su), slot)
-
-    out = []
-    u = 0
-    for g in range(grid):
-        lo, hi = range_lo(g), range_lo(g + 1)
-        while u + 1 < units and starts[u + 1] <= lo:
-            u += 1
-        s1, p1 = starts[u], pages[u // hkv]
-        i1 = i2 = None
-        if lo - s1 < p1:
-            i1 = item(u, lo, hi, 2 * g)
-        elif p1 == 0 and lo == s1:
-            i1 = item(u, lo, hi, 2 * g)
-        s2 = s1 + max(p1, t)
-        if s2 < hi:
-            i2 = item(u + 1, s2, hi, 2 * g + 1)
-        out.append((i1, i2))
-    return out

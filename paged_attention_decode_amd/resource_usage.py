@@ -34,11 +34,8 @@ FIELDS = {
 
 
 def _demangle_args(name: str) -> str:
-    # _ZN3pad17pad_phase1_kernelILi128ELi1ELi0ELi0ELb0EEEvNS_10Phase1ArgsE -> <128, 1, 0, 0>;
-    # ...ELb1EEE... (the stream kernel) -> <128, 1, 0, 0, S>
+    # _ZN3pad17pad_phase1_kernelILi128ELi1ELi0ELi0EEEvNS_10Phase1ArgsE -> <128, 1, 0, 0>
     args = re.findall(r"Li(\d+)E", name)
-    if re.search(r"Lb1E", name):
-        args.append("S")
     return "<" + ", ".join(args) + ">" if args else name
 
 

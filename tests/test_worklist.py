@@ -13,14 +13,10 @@ FlashInfer-style ``plan(indptr, indices, last_page_len, ...)`` /
 ``run(q, (k_cache, v_cache))`` surface is checked against the fp32 oracle
 on the cases of the reference's tests/test_flashinfer_adapter.py:34-136.
 
-The lists themselves are checked for structure (tests/plan_check.py): every
-(sequence, kv head) unit's pages are covered by its items exactly once and
-in order, an empty unit has the one item that writes its zero rows, each
-item owns the slot where its unit's merge looks for it (consecutive slots
-for per-unit items; slot 2g / 2g + 1 for the two stream items of workgroup
-g), and each wave's first page id is the table's.  On launches of the
-stream kernel the planner kernel's items must equal the Python restatement
-of the stream plan (heuristics.stream_items) field for field.
+The lists themselves are checked for structure: every (sequence, kv head)
+unit's pages are covered by its items exactly once and in order, an empty
+unit has the one item that writes its zero rows, the item slots of a unit
+are its own contiguous range, and each wave's first page id is the table's.
 
 CPU: the work-list size is a header plus one record per workgroup; the
 structure check rejects planted mistakes in a hand-built list.
@@ -36,12 +32,10 @@ import torch
 
 from oracle.reference import decode_fp16_protocol
 from paged_attention_decode_amd import _native
-from paged_attention_decode_amd import heuristics
 from tests.helpers import assert_parity, make_cache, shuffled_table
-from tests.plan_check import check_items
 
 WL_HEADER_BYTES = 128
-WL_RECORD_BYTES = 256  # two halves of 32 int32: item 1, item 2
+WL_RECORD_BYTES = 128
 
 
 # ---------------------------------------------------------------- CPU
@@ -261,56 +255,53 @@ def test_list_from_other_lengths_keeps_scratch_consistent():
 
 # ---------------------------------------------------------------- plan structure
 WL_INTS = WL_RECORD_BYTES // 4
-HALF = WL_INTS // 2
-HEADER_INTS = WL_HEADER_BYTES // 4
 
 
-def _decode_list(wl):
-    """(G, items per workgroup) of a list as int32 on the host; each item is
-    (fields..., record half): b, kvh, p_begin, p_end, L, nsplit, slot0, col_max, row, slot, sstride, odd, half."""
-    assert wl[0] == 0x574C4150
-    G = int(wl[2])
-    recs = wl[HEADER_INTS:HEADER_INTS + WL_INTS * G].view(G, WL_INTS)
-    out = []
-    for g in range(G):
-        its = []
-        for k in range(2):
-            r = recs[g, k * HALF:(k + 1) * HALF].tolist()
-            if r[8]:
-                its.append((r, k))
-            else:
-                assert all(x == 0 for x in r), (g, k)  # a half without an item is all zero
-        out.append(its)
-    return G, out
-
-
-def _check_plan_structure(wl, lens, ps, hkv, bt_rows, nw, max_pages, slots_per_group=1):
+def _check_plan_structure(wl, lens, ps, hkv, bt_rows, nw, max_pages):
     """The items a work list holds cover every (sequence, kv head) unit's pages exactly once.
 
     wl: the list as int32 on the host; lens: sequence lengths; bt_rows[b]: the
     page ids of sequence b in order (its row of the dense table, or its CSR
     slice); nw: waves per workgroup."""
-    G, groups = _decode_list(wl)
-    pages = [min(-(-L // ps), max_pages) for L in lens]
-    items = []
-    for g, its in enumerate(groups):
-        row = []
-        for r, k in its:
-            b, kvh, p0, p1, L, nsplit, slot0, col_max, _valid, _row, slot, sstride, odd = r[:13]
-            assert k == 0 or slots_per_group == 2, (g, k)
-            assert 0 <= b < len(lens) and L == lens[b], (g, r)
-            assert sstride == slots_per_group or sstride == 1, (g, r)
-            if nsplit:
-                assert col_max >= p1 - 1, (g, r)
-                if ps % 16 == 0:  # whole-page blocks: each wave's first page id is in the record
-                    for w in range(nw):
-                        if p0 * ps + w * 16 < min(p1 * ps, L):
-                            col = min(p0 + (w * 16) // ps, col_max)
-                            assert r[16 + w] == int(bt_rows[b][col]), (g, k, w)
-            row.append((b, kvh, p0, p1, nsplit, slot0, sstride, odd, slot))
-        items.append(row)
-    check_items(items, pages, hkv, slots_per_group)
-    return groups
+    assert wl[0] == 0x574C4150
+    G = int(wl[2])
+    recs = wl[WL_INTS:WL_INTS + WL_INTS * G].view(G, WL_INTS)
+    units = {}
+    for g in range(G):
+        r = recs[g].tolist()
+        b, kvh, p0, p1, L, nsplit, slot0, col_max, valid = r[:9]
+        if not valid:
+            continue
+        assert 0 <= b < len(lens) and 0 <= kvh < hkv and L == lens[b]
+        pages = min(-(-L // ps), max_pages)
+        units.setdefault((b, kvh), []).append((p0, p1, g, nsplit, slot0))
+        if pages == 0:
+            assert nsplit == 0
+            continue
+        assert 0 <= p0 < p1 <= pages and slot0 <= g < slot0 + nsplit and col_max >= p1 - 1
+        if ps % 16 == 0:  # whole-page blocks: each wave's first page id is in the record
+            for w in range(nw):
+                col = min(p0 + (w * 16) // ps, col_max)
+                assert r[16 + w] == int(bt_rows[b][col]), (g, w)
+    slots = []
+    for b, L in enumerate(lens):
+        pages = min(-(-L // ps), max_pages)
+        for kvh in range(hkv):
+            items = sorted(units.get((b, kvh), []))
+            if pages == 0:
+                assert len(items) == 1, (b, kvh)  # one workgroup writes the zero rows
+                continue
+            assert len(items) == items[0][3], (b, kvh)  # nsplit items
+            assert items[0][0] == 0 and items[-1][1] == pages, (b, kvh)
+            for (_, e, *_), (s, *_) in zip(items, items[1:]):
+                assert e == s, (b, kvh)  # contiguous, no overlap
+            slot0 = items[0][4]
+            assert all(it[4] == slot0 for it in items)
+            assert sorted(it[2] for it in items) == list(range(slot0, slot0 + len(items)))
+            slots.append((slot0, slot0 + len(items)))
+    slots.sort()
+    for (_, e), (s, _) in zip(slots, slots[1:]):
+        assert e <= s  # units' slot ranges are disjoint
 
 
 @pytest.mark.gpu
@@ -333,13 +324,12 @@ def test_work_list_covers_every_page_once(kind, ps, csr, d):
         ip = indptr.cpu().tolist()
         rows = [indices.cpu()[ip[b]:ip[b + 1]].tolist() for b in range(len(lens))]
         max_pages = 1 << 30
-        shape = pad.plan(len(lens), hkv * group, hkv, d, ps, max(indices.numel(), 1), csr=True)
+        nw = pad.plan(len(lens), hkv * group, hkv, d, ps, max(indices.numel(), 1), csr=True)["waves_per_group"]
     else:
         plan = lambda: ext().plan_worklist(bt, sl, hkv * group, hkv, d, ps, 0)  # noqa: E731
         rows = bt.cpu().tolist()
         max_pages = bt.shape[1]
-        shape = pad.plan(len(lens), hkv * group, hkv, d, ps, max_pages)
-    nw, spg = shape["waves_per_group"], shape["slots_per_group"]
+        nw = pad.plan(len(lens), hkv * group, hkv, d, ps, max_pages)["waves_per_group"]
     wl = plan()
     # Planning the same inputs again (into fresh memory) gives the same list
     # word for word, including the records of slots without an item.
@@ -348,82 +338,26 @@ def test_work_list_covers_every_page_once(kind, ps, csr, d):
     wl2 = plan()
     torch.cuda.synchronize()
     assert torch.equal(wl, wl2)
-    _check_plan_structure(wl.cpu().view(torch.int32), lens, ps, hkv, rows, nw, max_pages, spg)
+    _check_plan_structure(wl.cpu().view(torch.int32), lens, ps, hkv, rows, nw, max_pages)
 
 
-STREAM_CASES = [
-    # (lens kind or explicit lengths, hkv, group, head_dim, page_size)
-    ("ragged32", 2, 6, 128, 32),     # C3-like
-    ("ragged100", 1, 8, 128, 16),    # 4 sequences per lane
-    ([3000, 0, 5000, 0, 2000, 4000], 2, 6, 128, 16),  # empty sequences: zero-row owners
-    ("ragged32", 2, 6, 64, 16),
-    ([131072, 16], 2, 6, 128, 16),   # one unit over > 48 ranges: two-level merge of stream items
-    ([5000, 0, 3000, 1, 7000], 8, 4, 128, 16),
-]
-
-
-@pytest.mark.gpu
-@pytest.mark.parametrize("kind,hkv,group,d,ps", STREAM_CASES)
-def test_stream_list_equals_python_mirror(kind, hkv, group, d, ps):
-    import paged_attention_decode_amd as pad
-    from paged_attention_decode_amd._native import ext
-
-    lens = kind if isinstance(kind, list) else _lens(kind, 37)[0]
-    q, k, v, bt, sl = _dense_case(lens, hkv, group, d, ps, 37)
-    shape = pad.plan(len(lens), hkv * group, hkv, d, ps, bt.shape[1])
-    assert shape["slots_per_group"] == 2, shape
-    wl = ext().plan_worklist(bt, sl, hkv * group, hkv, d, ps, 0)
-    torch.cuda.synchronize()
-    G, groups = _decode_list(wl.cpu().view(torch.int32))
-    pages = [-(-L // ps) for L in lens]
-    mirror = heuristics.stream_items(pages, hkv, G, -(-256 // ps))
-    assert mirror is not None
-    for g, (its, (m1, m2)) in enumerate(zip(groups, mirror)):
-        want = {}
-        for k_, m in ((0, m1), (1, m2)):
-            if m is not None:
-                want[k_] = [m.b, m.kvh, m.p_begin, m.p_end, lens[m.b], m.nsplit, m.slot0, pages[m.b] - 1, 1, 0,
-                            m.slot, 2, m.odd]
-        got = {k_: r[:13] for r, k_ in its}
-        assert got == want, (g, got, want)
-    _check_plan_structure(wl.cpu().view(torch.int32), lens, ps, hkv, bt.cpu().tolist(), shape["waves_per_group"],
-                          bt.shape[1], 2)
-    # The planned run and the in-kernel plan agree bit for bit, and with the oracle.
-    w = pad.BatchDecodeWrapper()
-    w.plan_block_table(bt, sl, q.shape[1], hkv, d, ps)
-    out = w.run(q, (k, v))
-    ref = pad.paged_attention_decode(q, k, v, bt, sl)
-    torch.cuda.synchronize()
-    assert torch.equal(out, ref)
-    assert_parity(out, decode_fp16_protocol(q.float().cpu(), k.float().cpu(), v.float().cpu(), bt.cpu(), sl.cpu()))
-
-
-def _synthetic_list(stream=False):
-    # Two sequences of 5 and 0 pages (page size 16), one kv head.
-    # Per-unit items (4 workgroups): sequence 0 in items [0, 3) and [3, 5)
-    # (slots 0, 1), sequence 1's zero rows in slot 2, workgroup 3 without an
-    # item.  Stream items (2 workgroups, 4 slots): workgroup 0 holds pages
-    # [0, 3) (slot 0), workgroup 1 pages [3, 5) (slot 2) and, as its item 2,
-    # sequence 1's zero rows (slot 3).
-    G = 2 if stream else 4
-    wl = torch.zeros(HEADER_INTS + WL_INTS * G, dtype=torch.int32)
-    wl[0], wl[2] = 0x574C4150, G
+def _synthetic_list():
+    # Two sequences of 5 and 0 pages (page size 16), one kv head, 4 slots:
+    # sequence 0 in items [0, 3) and [3, 5) (slots 0, 1), sequence 1's zero
+    # rows in slot 2, slot 3 without an item.
+    wl = torch.zeros(WL_INTS * 5, dtype=torch.int32)
+    wl[0], wl[2] = 0x574C4150, 4
     rows = [[10, 11, 12, 13, 14, 15], [20, 21, 22, 23, 24, 25]]
 
-    def rec(g, half, vals, pids):
-        base = HEADER_INTS + WL_INTS * g + HALF * half
+    def rec(g, vals, pids):
+        base = WL_INTS * (1 + g)
         wl[base:base + len(vals)] = torch.tensor(vals, dtype=torch.int32)
         wl[base + 16:base + 16 + len(pids)] = torch.tensor(pids, dtype=torch.int32)
 
-    # b, kvh, p_begin, p_end, L, nsplit, slot0, col_max, valid, row, slot, sstride, odd
-    if stream:
-        rec(0, 0, [0, 0, 0, 3, 70, 2, 0, 5, 1, 0, 0, 2, 0], [10, 11])
-        rec(1, 0, [0, 0, 3, 5, 70, 2, 0, 5, 1, 0, 2, 2, 0], [13, 14])
-        rec(1, 1, [1, 0, 0, 0, 0, 0, 3, -1, 1, 0, 3, 2, 0], [])
-    else:
-        rec(0, 0, [0, 0, 0, 3, 70, 2, 0, 5, 1, 0, 0, 1, 0], [10, 11])
-        rec(1, 0, [0, 0, 3, 5, 70, 2, 0, 5, 1, 0, 1, 1, 0], [13, 14])
-        rec(2, 0, [1, 0, 0, 0, 0, 0, 2, -1, 1, 0, 2, 1, 0], [])
+    # b, kvh, p_begin, p_end, L, nsplit, slot0, col_max, valid, row
+    rec(0, [0, 0, 0, 3, 70, 2, 0, 5, 1, 0], [10, 11])
+    rec(1, [0, 0, 3, 5, 70, 2, 0, 5, 1, 0], [13, 14])
+    rec(2, [1, 0, 0, 0, 0, 0, 2, -1, 1, 0], [])
     return wl, rows
 
 
@@ -431,37 +365,16 @@ def test_plan_structure_check_catches_planted_mistakes():
     lens, ps, hkv, nw, max_pages = [70, 0], 16, 1, 2, 6
     wl, rows = _synthetic_list()
     _check_plan_structure(wl, lens, ps, hkv, rows, nw, max_pages)
-    r = lambda g, half=0: HEADER_INTS + WL_INTS * g + HALF * half  # noqa: E731
+    base = WL_INTS
     mistakes = [
-        (r(1) + 2, 2),   # second item starts inside the first: overlap
-        (r(1) + 3, 4),   # a page left uncovered at the end
-        (r(0) + 16, 12),  # wrong first page id of wave 0
-        (r(1) + 6, 1),   # inconsistent slot0 inside a unit
-        (r(1) + 10, 0),  # the item's slot is another workgroup's
-        (r(2) + 8, 0),   # the empty sequence's zero rows have no item
+        (base * 2 + 2, 2),   # second item starts inside the first: overlap
+        (base * 2 + 3, 4),   # a page left uncovered at the end
+        (base * 1 + 16, 12),  # wrong first page id of wave 0
+        (base * 2 + 6, 1),   # inconsistent slot0 inside a unit
+        (base * 3 + 8, 0),   # the empty sequence's zero rows have no item
     ]
     for idx, val in mistakes:
         bad = wl.clone()
         bad[idx] = val
         with pytest.raises(AssertionError):
             _check_plan_structure(bad, lens, ps, hkv, rows, nw, max_pages)
-
-
-def test_stream_plan_structure_check_catches_planted_mistakes():
-    lens, ps, hkv, nw, max_pages = [70, 0], 16, 1, 2, 6
-    wl, rows = _synthetic_list(stream=True)
-    _check_plan_structure(wl, lens, ps, hkv, rows, nw, max_pages, slots_per_group=2)
-    r = lambda g, half=0: HEADER_INTS + WL_INTS * g + HALF * half  # noqa: E731
-    mistakes = [
-        (r(1) + 10, 1),     # item 1 of workgroup 1 in workgroup 0's second slot
-        (r(1) + 2, 2),      # overlapping ranges of one unit
-        (r(0) + 12, 1),     # entry 0 offset set: the merge would look in slot 1
-        (r(1, 1) + 10, 2),  # item 2 in item 1's slot
-        (r(1, 1) + 8, 0),   # the empty sequence's zero rows have no owner
-        (r(1) + 17, 99),    # wrong first page id of wave 1
-    ]
-    for idx, val in mistakes:
-        bad = wl.clone()
-        bad[idx] = val
-        with pytest.raises(AssertionError):
-            _check_plan_structure(bad, lens, ps, hkv, rows, nw, max_pages, slots_per_group=2)
