@@ -58,6 +58,12 @@ What one run measures (one GPU; ``--gpus`` above 1 exits with a message):
   all layers), cold throughput.
 * ``c2_sweep[b].us_per_call_cold_planned``: the same plan-once-run-many
   timing for each batch of C2.
+* ``c2_fp8`` (``--no-fp8`` skips it): the headline step over fp8 K/V caches
+  (float8_e4m3fn and float8_e5m2 codes of the same C2 inputs, per-tensor
+  scales; ``paged_attention_decode_fp8``), cold throughput in GB/s of its
+  own algorithmic bytes (one byte per K/V element), the time ratio to the
+  fp16 headline, and batch 1 by the reference's latency method.  Not the
+  metric, which is quoted on fp16 caches.
 * ``cpu_baseline_configs`` (``--cpu-configs``, by default C1, C3, C4 and
   C5; ``none`` skips it): the CPU oracle next to the GPU call on each listed
   configuration in the same run, with the sample sizes the reference's bench
@@ -100,6 +106,7 @@ def _parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-ceiling", action="store_true", help="skip the measured read ceiling")
     p.add_argument("--no-ragged", action="store_true", help="skip the C3 ragged line")
+    p.add_argument("--no-fp8", action="store_true", help="skip the fp8-cache lines")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--cpu-threads", type=int, default=16,
                    help="most CPU threads for the baseline (a GPU box grants one GPU 16 cores)")
@@ -121,6 +128,9 @@ def _make_sets(make, n, **kw):
 
 
 def _call(pad, w, engine, splits):
+    if w.k_cache.element_size() == 1:  # fp8 caches (workloads.to_fp8)
+        return pad.paged_attention_decode_fp8(*w.args(), k_scale=w.k_scale, v_scale=w.v_scale,
+                                              num_splits=splits or None)
     return pad.paged_attention_decode_ex(*w.args(), num_splits=splits or None, engine=engine)
 
 
@@ -552,6 +562,33 @@ def main():
                 "pct_of_peak_planned": round(100 * nb3 / planned / 1e9 / PEAK_GBS, 2),
             })
         del rs, csr_args
+
+    if not args.no_fp8 and engine == 0:
+        # The headline step over fp8 caches (same C2 inputs converted, one byte
+        # per K/V element): not the metric, which is quoted on fp16 caches.
+        fp8 = {}
+        for fmt, dt in wl.FP8_NAMES.items():
+            first = wl.to_fp8(wl.make("C2", batch=args.batch, seed=1000), dt)
+            rs = [first] + [wl.to_fp8(wl.make("C2", batch=args.batch, seed=1000 + i), dt)
+                            for i in range(1, _rotation(first.k_cache.numel() * 2))]
+            t8 = _throughput(pad, rs, engine, splits, args.steps, args.warmup)
+            nb8 = wl.bytes_of(first)
+            w1 = wl.to_fp8(wl.make("C2", batch=1, seed=2001), dt)
+            lat1, _ = _latency_reference_method(pad, w1, engine, splits, max(3, args.trials // 3))
+            fp8[fmt] = {
+                "us_per_call_cold": round(t8 * 1e6, 2),
+                "gbs_cold": round(nb8 / t8 / 1e9, 1),
+                "pct_of_peak_cold": round(100 * nb8 / t8 / 1e9 / PEAK_GBS, 2),
+                "algorithmic_bytes_per_call": nb8,
+                "speedup_vs_fp16_headline": round(sec / t8, 3),
+                "b1_us_per_call_warm": round(lat1, 2),
+            }
+            del rs, first, w1
+        result["c2_fp8"] = {
+            "workload": f"C2 batch {args.batch} with fp8 K/V caches (per-tensor scales, codes spanning 7/8 of the "
+                        "range); cold rotation; q and output fp16",
+            **fp8,
+        }
 
     if not args.no_sweep:
         sweep = {}

@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PAD_ABI_VERSION 4
+#define PAD_ABI_VERSION 5
 
 /* Largest supported GQA group (query heads per KV head); the reference's
  * bound is the same (cuda/kernel_v4_split_k.cu:44). */
@@ -79,9 +79,17 @@ typedef enum pad_status {
   PAD_ERR_NUM_SPLITS = 8,        /* num_splits < 0 or > PAD_MAX_SPLITS     */
   PAD_ERR_LAUNCH = 9,            /* the HIP runtime rejected a launch      */
   PAD_ERR_DEVICE = 10,           /* no usable device / device query failed */
-  PAD_ERR_SCRATCH_LIMIT = 11     /* pad_decode_launch_noalloc: the call needs
+  PAD_ERR_SCRATCH_LIMIT = 11,    /* pad_decode_launch_noalloc: the call needs
                                     more than its static scratch holds      */
+  PAD_ERR_KV_FORMAT = 12         /* pad_decode_launch_kv8: unknown cache
+                                    format, or a scale that is not finite
+                                    and positive                            */
 } pad_status;
+
+/* Element formats of the K/V caches (pad_decode_launch_kv8). */
+#define PAD_KV_FP16 0         /* IEEE half (every other entry point)          */
+#define PAD_KV_FP8_E4M3FN 1   /* OCP fp8 E4M3 "fn": bias 7, no infinities     */
+#define PAD_KV_FP8_E5M2 2     /* OCP fp8 E5M2: bias 15, IEEE-like             */
 
 /* Static scratch of pad_decode_launch_noalloc(), per device: fp32 partials
  * and int32 arrival counters.  48 MiB in all, held until the process ends. */
@@ -207,6 +215,27 @@ int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache,
                       int32_t* counters, int64_t num_counters,
                       const pad_decode_dims* dims, float scale,
                       int num_splits, void* stream);
+
+/* pad_decode_launch() over fp8 K/V caches: k_cache / v_cache hold one byte
+ * per element in `kv_format` (PAD_KV_FP8_E4M3FN or PAD_KV_FP8_E5M2; the
+ * layouts, strides in elements = bytes, of the fp16 caches), and represent
+ * K = k_scale * k_cache and V = v_scale * v_cache (per-tensor scales, the
+ * convention of serving engines' fp8 KV caches).  q and out stay fp16;
+ * head_dim 64, 128 or 256.  Each element is widened to fp16 exactly in
+ * registers, so the result equals the fp16 path's on the dequantized
+ * caches up to fp32 rounding: k_scale goes into the softmax scale and
+ * v_scale into the output normalisation.  Same plan, workspace and
+ * counters as pad_decode_launch() (pad_decode_plan()).  No counterpart in
+ * the reference, whose caches are fp16 only (src/kernel_cuda_v4.py:37-48);
+ * it is the next data format of the same operator. */
+int pad_decode_launch_kv8(const void* q, const void* k_cache,
+                          const void* v_cache, const int32_t* block_table,
+                          const int32_t* seq_lens, void* out,
+                          void* workspace, size_t workspace_bytes,
+                          int32_t* counters, int64_t num_counters,
+                          const pad_decode_dims* dims, float scale,
+                          int kv_format, float k_scale, float v_scale,
+                          int num_splits, void* stream);
 
 /* Same as pad_decode_launch(), with the engine forced (0 = MFMA tiles,
  * 1 = VALU/DPP dot products) and, when `events` is not NULL, three

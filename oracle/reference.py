@@ -113,6 +113,23 @@ def decode_fp16_protocol(q, k_cache, v_cache, block_table, seq_lens, scale=None)
                                             seq_lens.detach().to("cpu"), scale)
 
 
+def decode_fp8_protocol(q, k_cache, v_cache, block_table, seq_lens, k_scale=1.0, v_scale=1.0, scale=None):
+    """Oracle for fp8 caches: the fp32 oracle on the dequantised caches.
+
+    k_cache / v_cache are torch.float8_e4m3fn or torch.float8_e5m2 holding
+    K / k_scale and V / v_scale (per-tensor scales); the oracle decodes each
+    code with PyTorch's float8 -> float32 conversion, multiplies by the
+    scale in fp32 and runs ``paged_attention_decode_reference`` on fp16-rounded
+    q.  The reference's caches are fp16 only (src/kernel_cuda_v4.py:37-48);
+    this extends its oracle to the dequantised values.
+    """
+    q32 = q.detach().to("cpu").half().float()
+    k32 = k_cache.detach().to("cpu").float() * float(k_scale)
+    v32 = v_cache.detach().to("cpu").float() * float(v_scale)
+    return paged_attention_decode_reference(q32, k32, v32, block_table.detach().to("cpu"),
+                                            seq_lens.detach().to("cpu"), scale)
+
+
 def decode_rows_fp16_protocol(q, k_cache, v_cache, block_table, seq_lens, rows, scale=None):
     """The oracle for a subset of batch rows, gathering only those rows' pages.
 

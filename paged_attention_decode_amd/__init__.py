@@ -9,11 +9,14 @@ from .ops import (  # noqa: F401
     BatchDecodeWrapper,
     ENGINE_MFMA,
     ENGINE_VALU,
+    FP8_CACHE_DTYPES,
+    FP8_HEAD_DIMS,
     SUPPORTED_HEAD_DIMS,
     paged_attention_decode,
     paged_attention_decode_csr,
     paged_attention_decode_cuda_v4,
     paged_attention_decode_ex,
+    paged_attention_decode_fp8,
     paged_kv_indices,
     plan,
 )
@@ -24,9 +27,12 @@ __all__ = [
     "paged_attention_decode_cuda_v4",
     "paged_attention_decode_ex",
     "paged_attention_decode_csr",
+    "paged_attention_decode_fp8",
     "paged_kv_indices",
     "plan",
     "ENGINE_MFMA",
     "ENGINE_VALU",
     "SUPPORTED_HEAD_DIMS",
+    "FP8_CACHE_DTYPES",
+    "FP8_HEAD_DIMS",
 ]

@@ -103,6 +103,11 @@ SIGNATURES = {
          ctypes.c_float, ctypes.c_int, _VP],
         ctypes.c_int,
     ),
+    "pad_decode_launch_kv8": (
+        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, _VP, ctypes.c_int64, ctypes.POINTER(PadDims),
+         ctypes.c_float, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int, _VP],
+        ctypes.c_int,
+    ),
     "pad_decode_launch_ex": (
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_size_t, _VP, ctypes.c_int64, ctypes.POINTER(PadDims),
          ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_VP), _VP],

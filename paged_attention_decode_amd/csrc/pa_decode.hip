@@ -120,6 +120,7 @@ struct Phase1Args {
   int pair_heads;  // 1: workgroups 8 apart take kv heads 2m and 2m+1 (see grid_pos)
   int wl_key;      // key of the launch's plan, matched against the work list's header
   float scale_log2;
+  float v_fix;     // fp8 caches: V's scale, applied to the output rows
   const int32_t* bt;      // dense: block_table [B, max_pages]; CSR: indices
   const int32_t* sl;      // dense: seq_lens [B]
   const int32_t* indptr;  // CSR: [B + 1] offsets of each sequence's page ids in bt
@@ -367,11 +368,14 @@ __device__ __forceinline__ int clamp_page(int phys, int64_t num_pages) {
 template <int D>
 constexpr int wave_row_floats() { return D + 4; }
 
-// One 16-token block of K and V in registers, in the MFMA operand layouts.
-template <int D>
+// One 16-token block of K and V in registers as loaded: lane (g, r16) holds
+// its D/16 elements of token 4g+i (fp16: D/32 dwords; fp8 caches: D/64
+// dwords of codes, widened to fp16 only where compute() uses them, so that
+// the loads of the next block stay in flight across the current one).
+template <int D, int ES = 2>
 struct KVTile {
-  HVec<D / 32> k[4];    // K[token 4g+i][r16*(D/16) + 0..D/16-1]
-  HVec<D / 32> v[4];    // V[token 4g+i][r16*(D/16) + 0..D/16-1]
+  HVec<D * ES / 64> k[4];
+  HVec<D * ES / 64> v[4];
 };
 
 // Bytes per token row of a wave's K staging tile in LDS (16 rows): the row
@@ -404,6 +408,38 @@ constexpr int kModeGeneric = 0;
 constexpr int kModeUniform = 1;
 constexpr int kModeSubpage = 2;
 
+// Element formats of the K/V caches (template parameter KVF of the MFMA
+// engine): fp16, or an OCP fp8 format, widened to fp16 in registers where
+// compute() uses a block, so that everything downstream (K staging, both
+// MFMAs, the softmax) is the fp16 path.
+constexpr int kKvF16 = 0;
+constexpr int kKvE4M3 = 1;  // float8_e4m3fn
+constexpr int kKvE5M2 = 2;  // float8_e5m2
+
+template <int KVF>
+constexpr int kv_elem_bytes() { return KVF == kKvF16 ? 2 : 1; }
+
+// Four fp8 codes (one dword, element i in byte i) as four fp16 values (two
+// dwords: elements 0-1 in lo, 2-3 in hi) with gfx950's scaled conversions
+// (v_cvt_scalef32_pk_f16_fp8 / _bf8, one per pair).  Their scale operand
+// acts through its exponent only, so it is 1 here and the launch folds the
+// caller's k_scale / v_scale into the softmax scale and the output
+// normalisation.  At scale 1 every code converts exactly, NaN codes to fp16
+// NaNs (every e4m3fn value and every e5m2 value is an fp16 value).
+template <int KVF>
+__device__ __forceinline__ void fp8x4_to_f16x4(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  h2_t a, b;
+  if constexpr (KVF == kKvE4M3) {
+    a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
+    b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true);
+  } else {
+    a = __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, false);
+    b = __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, true);
+  }
+  lo = __builtin_bit_cast(uint32_t, a);
+  hi = __builtin_bit_cast(uint32_t, b);
+}
+
 // head_dim 256 keeps the Q^T operand in LDS instead of 32 VGPRs per lane
 // (with it in registers the kernel spilled 25-38 VGPRs to scratch inside
 // the streaming loop).  One padded 16-row copy per workgroup: every lane
@@ -412,7 +448,7 @@ constexpr int kModeSubpage = 2;
 template <int D>
 constexpr bool q_in_lds() { return D >= 256; }
 
-template <int D, int MODE>
+template <int D, int MODE, int KVF = kKvF16>
 __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_first, const int32_t* bt_row,
                                                int64_t ids_stride, int b, int kvh, int t_begin, int t_end,
                                                int nblk, int wave, int nw, int lane, float2* sm_ml, float* sm_o,
@@ -420,6 +456,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   constexpr int DK = D / 32;  // 16-byte K chunks per lane per token
   constexpr int DT = D / 16;  // PV output tiles; V halves per lane per token
   constexpr int NDW = DT / 2;
+  constexpr int ES = kv_elem_bytes<KVF>();  // bytes per cache element
+  static_assert(KVF == kKvF16 || NDW % 2 == 0, "fp8 caches: head_dim a multiple of 64");
   // A lane's DT halves of a token row are NSEG segments of SEG dwords, so
   // that the 16 lanes of a group read 16*SEG*4 contiguous bytes per load
   // instruction: half dt is head_dim slot dim(r16, dt) =
@@ -429,8 +467,21 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   constexpr int SEG = NDW > 4 ? 4 : NDW;
   constexpr int NSEG = NDW / SEG;
   constexpr int SEG_HALVES = D / NSEG;  // head_dim distance between segments
-  auto load_slice = [](const char* p) -> HVec<NDW> {
-    if constexpr (NSEG == 1) {
+  // Dwords per lane per token row as loaded (fp8: half of NDW).
+  constexpr int NDWR = NDW * ES / 2;
+  using Tile = KVTile<D, ES>;
+  auto load_slice = [](const char* p) -> HVec<NDWR> {
+    if constexpr (KVF != kKvF16) {
+      // fp8: the same segments at one byte per element, kept as codes.
+      HVec<NDWR> r;
+#pragma unroll
+      for (int sg = 0; sg < NSEG; ++sg) {
+        const HVec<SEG / 2> x = load_hvec_stream<SEG / 2>(reinterpret_cast<const _Float16*>(p + sg * SEG_HALVES));
+#pragma unroll
+        for (int w = 0; w < SEG / 2; ++w) r.w[sg * (SEG / 2) + w] = x.w[w];
+      }
+      return r;
+    } else if constexpr (NSEG == 1) {
       return load_hvec_stream<NDW>(reinterpret_cast<const _Float16*>(p));
     } else {
       HVec<NDW> r;
@@ -440,6 +491,17 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
 #pragma unroll
         for (int w = 0; w < SEG; ++w) r.w[sg * SEG + w] = x.w[w];
       }
+      return r;
+    }
+  };
+  // A loaded row in the fp16 layout (fp8 codes: four per dword, widened).
+  auto widen = [](const HVec<NDWR>& x) -> HVec<NDW> {
+    if constexpr (KVF == kKvF16) {
+      return x;
+    } else {
+      HVec<NDW> r;
+#pragma unroll
+      for (int w = 0; w < NDWR; ++w) fp8x4_to_f16x4<KVF>(x.w[w], r.w[2 * w], r.w[2 * w + 1]);
       return r;
     }
   };
@@ -470,8 +532,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = (f4_t)0.f;
 
-  const char* k_head = reinterpret_cast<const char*>(a.k + (int64_t)kvh * a.skh);
-  const char* v_head = reinterpret_cast<const char*>(a.v + (int64_t)kvh * a.svh);
+  const char* k_head = reinterpret_cast<const char*>(a.k) + (int64_t)kvh * a.skh * ES;
+  const char* v_head = reinterpret_cast<const char*>(a.v) + (int64_t)kvh * a.svh * ES;
   // Lane byte offsets inside a 16-token slab of one page (loop invariant).
   // K and V are both read as whole token rows: lane (g, r16) reads row
   // 4g+i, segments at head_dim r16*2*SEG (+ D/NSEG), so one load
@@ -485,8 +547,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = MODE >= kModeSubpage ? (4 * g + i) & ((1 << SUB_SHIFT) - 1) : 4 * g + i;
-    koff[i] = (uint32_t)(((int64_t)row * a.sks + r16 * 2 * SEG) * 2);
-    voff[i] = (uint32_t)(((int64_t)row * a.svs + r16 * 2 * SEG) * 2);
+    koff[i] = (uint32_t)(((int64_t)row * a.sks + r16 * 2 * SEG) * ES);
+    voff[i] = (uint32_t)(((int64_t)row * a.svs + r16 * 2 * SEG) * ES);
   }
   constexpr int KROW = k_stage_row_bytes<D>();
   const int p_first = page_of(a, t_begin);
@@ -530,7 +592,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   // order wave, wave+nw, ...; past the split the last block's id is reread).
   int pid_next = phys_first;
 
-  auto load = [&](KVTile<D>& t, int jb) {
+  auto load = [&](Tile& t, int jb) {
     if constexpr (MODE == kModeUniform) {
       // page_size % 16 == 0 and splits start on page boundaries: the block
       // lives in one page, so its page id and base address are wave-uniform.
@@ -539,8 +601,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
       const int phys = clamp_page(pid_next, a.num_pages);
       const int page_after = p_first + block_page(a, min(jb + nw, nblk - 1));
       pid_next = load_uniform_i32(bt_row + (int64_t)page_after * ids_stride);
-      const char* kb = k_head + ((int64_t)phys * a.skp + (int64_t)slot0 * a.sks) * 2;
-      const char* vb = v_head + ((int64_t)phys * a.svp + (int64_t)slot0 * a.svs) * 2;
+      const char* kb = k_head + ((int64_t)phys * a.skp + (int64_t)slot0 * a.sks) * ES;
+      const char* vb = v_head + ((int64_t)phys * a.svp + (int64_t)slot0 * a.svs) * ES;
 #pragma unroll
       for (int i = 0; i < 4; ++i) t.k[i] = load_slice(kb + koff[i]);
 #pragma unroll
@@ -554,7 +616,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
       // same registers.
 #pragma unroll
       for (int k = 0; k < SUB_PAGES; ++k) ids_next[k] = clamp_page(ids_next[k], a.num_pages);
-      const int64_t kpage = a.skp * 2, vpage = a.svp * 2;
+      const int64_t kpage = a.skp * ES, vpage = a.svp * ES;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int c0 = ids_next[i >> SUB_SHIFT], c1 = ids_next[(4 + i) >> SUB_SHIFT];
@@ -587,8 +649,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
         const int p45 = b0 ? ids_next[5] : ids_next[4];
         const int p03 = (idx & 2) ? p23 : p01;
         const int phys = (idx & 4) ? p45 : p03;
-        const char* kr = k_head + ((int64_t)phys * a.skp + (int64_t)slot * a.sks + r16 * 2 * SEG) * 2;
-        const char* vr = v_head + ((int64_t)phys * a.svp + (int64_t)slot * a.svs + r16 * 2 * SEG) * 2;
+        const char* kr = k_head + ((int64_t)phys * a.skp + (int64_t)slot * a.sks + r16 * 2 * SEG) * ES;
+        const char* vr = v_head + ((int64_t)phys * a.svp + (int64_t)slot * a.svs + r16 * 2 * SEG) * ES;
         t.k[i] = load_slice(kr);
         t.v[i] = load_slice(vr);
       }
@@ -596,7 +658,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
     }
   };
 
-  auto compute = [&](KVTile<D>& t, int jb) {
+  auto compute = [&](Tile& t, int jb) {
     const int t0 = t_begin + jb * kBlockTokens;
     const bool full = t0 + kBlockTokens <= t_end;
     // K rows -> LDS (row 4g+i, the lane's segments), then the MFMA A operand back
@@ -606,8 +668,9 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t* dst = reinterpret_cast<uint32_t*>(k_stage + (4 * g + i) * KROW + r16 * SEG * 4);
+      const HVec<NDW> kr = widen(t.k[i]);
 #pragma unroll
-      for (int w = 0; w < NDW; ++w) dst[(w / SEG) * (SEG_HALVES / 2) + w % SEG] = t.k[i].w[w];
+      for (int w = 0; w < NDW; ++w) dst[(w / SEG) * (SEG_HALVES / 2) + w % SEG] = kr.w[w];
     }
     h8_t kk[DK];
 #pragma unroll
@@ -665,11 +728,14 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
       psum += (float)p;  // l accumulates the same rounded weights P.V uses
     }
     l_run += psum;
+    HVec<NDW> vr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vr[i] = widen(t.v[i]);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       h4_t av;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = t.v[i].h(dt);
+      for (int i = 0; i < 4; ++i) av[i] = vr[i].h(dt);
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, o[dt], 0, 0, 0);
     }
   };
@@ -679,7 +745,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   // (no control-flow join on the in-flight registers); the last one or two
   // blocks are peeled.
   const int n_mine = wave < nblk ? (nblk - wave + nw - 1) / nw : 0;
-  KVTile<D> ta, tb;
+  Tile ta, tb;
   if (n_mine > 0) {
     int it = 0;
     fetch_ids(wave);
@@ -1338,8 +1404,9 @@ __global__ __launch_bounds__(64) void pad_plan_kernel(const Phase1Args a, int32_
   if (g == 0 && lane < kWlHeaderInts) wl[lane] = lane == 0 ? kWlMagic : (lane == 1 ? a.wl_key : (lane == 2 ? G : 0));
 }
 
-// Phase 1: one workgroup per (split, kv head, sequence).
-template <int D, int MODE, int ENGINE, int GQA_T>
+// Phase 1: one workgroup per (split, kv head, sequence).  KVF: the caches'
+// element format (fp16, or fp8 on the MFMA engine).
+template <int D, int MODE, int ENGINE, int GQA_T, int KVF = kKvF16>
 __global__ __launch_bounds__(max_group_waves(D) * 64)
     __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE, MODE))))
 void pad_phase1_kernel(const Phase1Args a) {
@@ -1423,9 +1490,9 @@ void pad_phase1_kernel(const Phase1Args a) {
   const int nblk = (t_end - t_begin + kBlockTokens - 1) / kBlockTokens;
 
   if constexpr (ENGINE == 0) {
-    wave_loop_mfma<D, MODE>(a, phys_first, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw,
-                               lane, sm_ml, sm_o, k_stage_all + wave * k_stage_bytes<D>(),
-                               k_stage_all + nw * k_stage_bytes<D>());
+    wave_loop_mfma<D, MODE, KVF>(a, phys_first, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave,
+                                 nw, lane, sm_ml, sm_o, k_stage_all + wave * k_stage_bytes<D>(),
+                                 k_stage_all + nw * k_stage_bytes<D>());
   } else {
     wave_loop_valu<D, MODE == kModeUniform, GQA_T>(a, it.ids_row, it.ids_stride, b, kvh, t_begin, t_end, nblk, wave, nw, lane,
                                       sm_ml, sm_o);
@@ -1472,7 +1539,8 @@ void pad_phase1_kernel(const Phase1Args a) {
       }
     }
     if (nsplit == 1) {
-      const float inv = 1.f / Ls;  // Ls >= 1: the max token contributes 2^0
+      // Ls >= 1: the max token contributes 2^0.  fp8 caches: V's scale too.
+      const float inv = (KVF != kKvF16 ? a.v_fix : 1.f) / Ls;
       h4_t hv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
@@ -1560,7 +1628,7 @@ void pad_phase1_kernel(const Phase1Args a) {
     float m = kNegInf, l = 0.f;
     f4_t acc = (f4_t)0.f;
     merge_partials(o_rsrc, ml_rsrc, 0, count, stride, gqa, row, col, D, m, l, acc);
-    const float inv = 1.f / l;
+    const float inv = (KVF != kKvF16 ? a.v_fix : 1.f) / l;
     h4_t hv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
@@ -1668,8 +1736,9 @@ static bool latency_bound_shape(const pad_decode_dims* d, int num_cus, bool csr)
   return units * blocks_per_seq <= 16 * (int64_t)num_cus;
 }
 
+// kv_bytes: bytes per K/V element (2 for fp16, 1 for fp8 caches).
 static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int engine, bool csr,
-                     pad_decode_plan_t* p) {
+                     pad_decode_plan_t* p, int kv_bytes = 2) {
   const int st = validate_dims(d);
   if (st != PAD_OK) return st;
   if (num_splits < 0 || num_splits > PAD_MAX_SPLITS) return PAD_ERR_NUM_SPLITS;
@@ -1729,13 +1798,15 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   // workgroup LDS budget allows.
   const int64_t split_tokens = (int64_t)pps * d->page_size;
   int nw = (int)((split_tokens + kBlockTokens - 1) / kBlockTokens);
-  // Bandwidth-bound shapes run 4 waves per workgroup, except head_dim <= 64
-  // with at most one (sequence, kv head) unit per CU: its 16-token tiles are
-  // half the bytes or less, and 8 waves keep as many bytes in flight per CU
-  // (32/8 d64 batch 32: 25.8 against 29.9 us; 16/4 d32: 17.8 against 21.9
-  // us).  With more units than CUs, 4-wave workgroups let several units
-  // share a CU (16/16 d64 batch 32: 46.9 against 47.9 us).
-  const bool narrow_rows = d->head_dim <= 64 && units <= num_cus;
+  // Bandwidth-bound shapes run 4 waves per workgroup, except rows of at
+  // most 128 bytes (fp16 head_dim <= 64, fp8 head_dim <= 128) with at most
+  // one (sequence, kv head) unit per CU: their 16-token tiles are half the
+  // bytes or less, and 8 waves keep as many bytes in flight per CU (32/8 d64
+  // batch 32: 25.8 against 29.9 us; 16/4 d32: 17.8 against 21.9 us).  With
+  // more units than CUs, 4-wave workgroups let several units share a CU
+  // (16/16 d64 batch 32: 46.9 against 47.9 us).  The split count does not
+  // depend on kv_bytes, so the scratch sizes do not either.
+  const bool narrow_rows = d->head_dim * kv_bytes <= 128 && units <= num_cus;
   const int nw_max = (latency_bound || narrow_rows) ? kMaxWaves : kMaxWaves / 2;
   if (nw > nw_max) nw = nw_max;
   const int cap = lds_wave_cap(gqa, d->head_dim, engine);
@@ -1773,10 +1844,35 @@ static int device_cus(int* out) {
   return PAD_OK;
 }
 
-template <int D, int MODE, int ENGINE, int GQA_T>
+template <int D, int MODE, int ENGINE, int GQA_T, int KVF = kKvF16>
 static hipError_t launch_p1(const Phase1Args& a, dim3 grid, int nw, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((pad_phase1_kernel<D, MODE, ENGINE, GQA_T>), grid, dim3(nw * 64), lds, st, a);
+  hipLaunchKernelGGL((pad_phase1_kernel<D, MODE, ENGINE, GQA_T, KVF>), grid, dim3(nw * 64), lds, st, a);
   return hipGetLastError();
+}
+
+// fp8 caches (MFMA engine; head_dim 64, 128 or 256): block mode from the
+// page size, as for fp16.
+template <int D, int KVF>
+static hipError_t dispatch_fp8(const Phase1Args& a, dim3 grid, int nw, size_t lds, hipStream_t st) {
+  if (a.ps % kBlockTokens == 0) return launch_p1<D, kModeUniform, 0, 0, KVF>(a, grid, nw, lds, st);
+  switch (a.ps) {
+    case 1: return launch_p1<D, kModeSubpage + 0, 0, 0, KVF>(a, grid, nw, lds, st);
+    case 2: return launch_p1<D, kModeSubpage + 1, 0, 0, KVF>(a, grid, nw, lds, st);
+    case 4: return launch_p1<D, kModeSubpage + 2, 0, 0, KVF>(a, grid, nw, lds, st);
+    case 8: return launch_p1<D, kModeSubpage + 3, 0, 0, KVF>(a, grid, nw, lds, st);
+    default: break;
+  }
+  return launch_p1<D, kModeGeneric, 0, 0, KVF>(a, grid, nw, lds, st);
+}
+
+template <int KVF>
+static hipError_t dispatch_fp8_dim(const Phase1Args& a, int head_dim, dim3 grid, int nw, size_t lds, hipStream_t st) {
+  switch (head_dim) {
+    case 64: return dispatch_fp8<64, KVF>(a, grid, nw, lds, st);
+    case 128: return dispatch_fp8<128, KVF>(a, grid, nw, lds, st);
+    case 256: return dispatch_fp8<256, KVF>(a, grid, nw, lds, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int D, int MODE>
@@ -1845,7 +1941,7 @@ static int plan_key(const Phase1Args& a) {
 static int setup_launch(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
                         const int32_t* indptr, const int32_t* lpl, void* out, void* ws, size_t ws_bytes,
                         int32_t* counters, int64_t num_counters, const pad_decode_dims* d, float scale,
-                        int num_splits, int engine, bool io, Launch* L) {
+                        int num_splits, int engine, bool io, Launch* L, int kv_bytes = 2) {
   if (engine != 0 && engine != 1) return PAD_ERR_INVALID_SHAPE;
   // Page ids are bounds-checked against num_pages on the device (an id
   // outside [0, num_pages) reads page 0), so a launch that reads pages needs
@@ -1856,7 +1952,7 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   if (st != PAD_OK) return st;
   const bool csr = indptr != nullptr || lpl != nullptr;
   pad_decode_plan_t& plan = L->plan;
-  st = plan_impl(d, num_splits, cus, engine, csr, &plan);
+  st = plan_impl(d, num_splits, cus, engine, csr, &plan, kv_bytes);
   if (st != PAD_OK) return st;
   const int gqa = d->num_q_heads / d->num_kv_heads;
   if (engine == 1 && !valu_supported(d->head_dim, gqa)) return PAD_ERR_UNSUPPORTED_GQA;
@@ -1929,6 +2025,7 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   for (int sh = 0; sh < 31; ++sh)
     if ((1 << sh) == d->page_size) a.ps_shift = sh;
   a.scale_log2 = scale * kLog2e;
+  a.v_fix = 1.0f;
   a.nw = plan.waves_per_group;
   a.wl_key = plan_key(a);
 #ifdef PAD_TIMELINE
@@ -1946,15 +2043,30 @@ static size_t worklist_bytes_for(const pad_decode_plan_t& plan, const pad_decode
   return sizeof(int32_t) * (size_t)(kWlHeaderInts + kWlRecordInts * G);
 }
 
+// kv_format: PAD_KV_FP16, or an fp8 format with per-tensor scales k_scale,
+// v_scale (the caches hold K / k_scale and V / v_scale).
 static int launch_impl(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
                        const int32_t* indptr, const int32_t* lpl, void* out, void* ws, size_t ws_bytes,
                        int32_t* counters, int64_t num_counters, const pad_decode_dims* d, float scale,
                        int num_splits, int engine, void* const* events, void* stream,
-                       const void* worklist = nullptr, size_t worklist_bytes = 0) {
+                       const void* worklist = nullptr, size_t worklist_bytes = 0, int kv_format = PAD_KV_FP16,
+                       float k_scale = 1.0f, float v_scale = 1.0f) {
+  if (kv_format != PAD_KV_FP16) {
+    if (kv_format != PAD_KV_FP8_E4M3FN && kv_format != PAD_KV_FP8_E5M2) return PAD_ERR_KV_FORMAT;
+    if (engine != 0) return PAD_ERR_KV_FORMAT;
+    if (d && d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return PAD_ERR_UNSUPPORTED_HEAD_DIM;
+    if (!(k_scale > 0.0f) || !(v_scale > 0.0f) || k_scale > 1.0e30f || v_scale > 1.0e30f) return PAD_ERR_KV_FORMAT;
+  }
   Launch L;
   int st = setup_launch(q, k, v, bt, sl, indptr, lpl, out, ws, ws_bytes, counters, num_counters, d, scale,
-                        num_splits, engine, true, &L);
+                        num_splits, engine, true, &L, kv_format == PAD_KV_FP16 ? 2 : 1);
   if (st != PAD_OK || L.empty) return st;
+  if (kv_format != PAD_KV_FP16) {
+    // The caches hold K / k_scale and V / v_scale: k_scale multiplies every
+    // score, v_scale every output row.
+    L.a.scale_log2 *= k_scale;
+    L.a.v_fix = v_scale;
+  }
   if (worklist != nullptr) {
     if (worklist_bytes < worklist_bytes_for(L.plan, d)) return PAD_ERR_WORKSPACE;
     L.a.worklist = static_cast<const int32_t*>(worklist);
@@ -1966,7 +2078,11 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   if (events && events[0] && hipEventRecord(reinterpret_cast<hipEvent_t>(events[0]), hs) != hipSuccess)
     return PAD_ERR_LAUNCH;
   hipError_t e;
-  switch (d->head_dim) {
+  if (kv_format == PAD_KV_FP8_E4M3FN) {
+    e = dispatch_fp8_dim<kKvE4M3>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
+  } else if (kv_format == PAD_KV_FP8_E5M2) {
+    e = dispatch_fp8_dim<kKvE5M2>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
+  } else switch (d->head_dim) {
     case 32: e = dispatch_phase1<32>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
     case 64: e = dispatch_phase1<64>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
     case 96: e = dispatch_phase1<96>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
@@ -2120,6 +2236,16 @@ int pad_decode_launch_ex(const void* q, const void* k_cache, const void* v_cache
                           workspace_bytes, counters, num_counters, dims, scale, num_splits, engine, events, stream);
 }
 
+int pad_decode_launch_kv8(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                          const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
+                          int32_t* counters, int64_t num_counters, const pad_decode_dims* dims, float scale,
+                          int kv_format, float k_scale, float v_scale, int num_splits, void* stream) {
+  if (kv_format == PAD_KV_FP16) return PAD_ERR_KV_FORMAT;  // fp16 caches: pad_decode_launch
+  return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, nullptr, nullptr, out, workspace,
+                          workspace_bytes, counters, num_counters, dims, scale, num_splits, 0, nullptr, stream,
+                          nullptr, 0, kv_format, k_scale, v_scale);
+}
+
 int pad_decode_launch_noalloc(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                               const int32_t* seq_lens, void* out, const pad_decode_dims* dims, float scale,
                               int num_splits, void* stream) {
@@ -2204,6 +2330,9 @@ const char* pad_status_string(int status) {
     case PAD_ERR_SCRATCH_LIMIT:
       return "the call needs more split scratch than pad_decode_launch_noalloc's static buffer holds "
              "(PAD_NOALLOC_WORKSPACE_BYTES of partials, PAD_NOALLOC_COUNTERS counters); use pad_decode_launch";
+    case PAD_ERR_KV_FORMAT:
+      return "unsupported K/V cache format or scale (fp8: PAD_KV_FP8_E4M3FN or PAD_KV_FP8_E5M2, MFMA engine, "
+             "finite positive k_scale and v_scale)";
     default: return "unknown status";
   }
 }

@@ -12,6 +12,8 @@
 // plan_worklist / plan_worklist_csr and forward_worklist / forward_worklist_csr
 // split a decode into a plan (once per decode step) and runs (once per
 // layer) over pad_decode_plan_worklist / pad_decode_launch_worklist.
+// forward_kv8 decodes over fp8 (e4m3fn / e5m2) caches through
+// pad_decode_launch_kv8.
 // Argument errors surface as RuntimeError (the reference used TORCH_CHECK,
 // cuda/kernel_v4_split_k.cu:216-223).  No host synchronisation.
 
@@ -121,18 +123,24 @@ void fill_dims(const torch::Tensor& q, const torch::Tensor& k, const torch::Tens
   for (int i = 0; i < 3; ++i) d->out_stride[i] = out.stride(i);
 }
 
-torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
-                      torch::Tensor block_table, torch::Tensor seq_lens, double scale,
-                      int64_t num_splits, int64_t engine) {
+// Checks shared by the dense-table entries; the caches hold cache_dtype.
+void check_dense(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache,
+                 const torch::Tensor& block_table, const torch::Tensor& seq_lens, at::ScalarType cache_dtype) {
   TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && block_table.is_cuda() &&
                   seq_lens.is_cuda(),
               "pa_decode: all tensors must be on the GPU");
   TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() &&
                   q.device() == block_table.device() && q.device() == seq_lens.device(),
               "pa_decode: all tensors must be on the same device");
-  TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
-                  v_cache.scalar_type() == at::kHalf,
-              "pa_decode: q, k_cache and v_cache must be float16");
+  if (cache_dtype == at::kHalf) {
+    TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
+                    v_cache.scalar_type() == at::kHalf,
+                "pa_decode: q, k_cache and v_cache must be float16");
+  } else {
+    TORCH_CHECK(q.scalar_type() == at::kHalf, "pa_decode: q must be float16");
+    TORCH_CHECK(k_cache.scalar_type() == cache_dtype && v_cache.scalar_type() == cache_dtype,
+                "pa_decode: k_cache and v_cache must both be float8_e4m3fn or both float8_e5m2");
+  }
   TORCH_CHECK(block_table.scalar_type() == at::kInt && seq_lens.scalar_type() == at::kInt,
               "pa_decode: block_table and seq_lens must be int32");
   TORCH_CHECK(q.dim() == 3, "pa_decode: q must be [batch, num_q_heads, head_dim]");
@@ -142,7 +150,12 @@ torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_ca
               "pa_decode: block_table must be [batch, max_pages]");
   TORCH_CHECK(seq_lens.dim() == 1 && seq_lens.size(0) == q.size(0), "pa_decode: seq_lens must be [batch]");
   TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
+}
 
+torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                      torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                      int64_t num_splits, int64_t engine) {
+  check_dense(q, k_cache, v_cache, block_table, seq_lens, at::kHalf);
   c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
   auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
   pad_decode_dims d;
@@ -164,6 +177,43 @@ torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_ca
                             block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
                             ws_ptr, plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
                             static_cast<int>(num_splits), static_cast<int>(engine), nullptr, stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return out;
+}
+
+// Decode over fp8 caches (torch.float8_e4m3fn or torch.float8_e5m2, both
+// caches the same) holding K / k_scale and V / v_scale; q and the output
+// stay fp16.  Same plan, scratch and stream as forward().
+torch::Tensor forward_kv8(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                          torch::Tensor block_table, torch::Tensor seq_lens, double scale, double k_scale,
+                          double v_scale, int64_t num_splits) {
+  const at::ScalarType kt = k_cache.scalar_type();
+  TORCH_CHECK(kt == at::kFloat8_e4m3fn || kt == at::kFloat8_e5m2,
+              "pa_decode: forward_kv8 needs float8_e4m3fn or float8_e5m2 caches");
+  check_dense(q, k_cache, v_cache, block_table, seq_lens, kt);
+  const int fmt = kt == at::kFloat8_e4m3fn ? PAD_KV_FP8_E4M3FN : PAD_KV_FP8_E5M2;
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+  pad_decode_dims d;
+  fill_dims(q, k_cache, v_cache, block_table, seq_lens, out, &d);
+
+  const int cus = cached_cus(q.get_device());
+  pad_decode_plan_t plan;
+  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cus, &plan);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  void* ws_ptr = nullptr;
+  int32_t* counters = nullptr;
+  if (!plan.single_pass) {
+    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
+    ws_ptr = sc.workspace.data_ptr();
+    counters = sc.counters.data_ptr<int32_t>();
+  }
+  st = pad_decode_launch_kv8(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                             block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
+                             ws_ptr, plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
+                             fmt, static_cast<float>(k_scale), static_cast<float>(v_scale),
+                             static_cast<int>(num_splits), stream);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   return out;
 }
@@ -461,6 +511,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward", &forward, "Paged-attention decode (q, k_cache, v_cache, block_table, seq_lens, scale, "
                              "num_splits, engine) -> out");
   m.def("forward_v4", &forward_v4, "Paged-attention decode with the reference forward_v4 argument list");
+  m.def("forward_kv8", &forward_kv8,
+        "Paged-attention decode over fp8 caches (q, k_cache, v_cache, block_table, seq_lens, scale, k_scale, "
+        "v_scale, num_splits) -> out");
   m.def("forward_csr", &forward_csr,
         "Paged-attention decode over a CSR page index (q, k_cache, v_cache, indptr, indices, last_page_len, "
         "scale, num_splits, engine) -> out");

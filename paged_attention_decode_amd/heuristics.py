@@ -68,8 +68,11 @@ def pages_per_seq(batch: int, max_pages: int, csr: bool) -> int:
 
 
 def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int, max_pages: int,
-         num_splits: int = 0, num_cus: int = 256, engine: int = 0, csr: bool = False) -> Plan:
-    """Same result as ``pad_decode_plan`` (``pad_decode_plan_csr`` with ``csr``) for valid arguments."""
+         num_splits: int = 0, num_cus: int = 256, engine: int = 0, csr: bool = False, kv_bytes: int = 2) -> Plan:
+    """Same result as ``pad_decode_plan`` (``pad_decode_plan_csr`` with ``csr``) for valid arguments.
+
+    ``kv_bytes=1`` gives the plan of an fp8-cache launch (pad_decode_launch_kv8): the same splits and
+    scratch, 8-wave workgroups for its 128-byte rows at head_dim 128."""
     if num_cus <= 0:
         num_cus = 256
     gqa = num_q_heads // num_kv_heads
@@ -98,7 +101,7 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
         pps = _cdiv(mp, want)
         s = _cdiv(mp, pps)
     nw = _cdiv(pps * page_size, BLOCK_TOKENS)
-    narrow_rows = head_dim <= 64 and units <= num_cus
+    narrow_rows = head_dim * kv_bytes <= 128 and units <= num_cus
     nw = min(nw, MAX_WAVES if latency_bound or narrow_rows else MAX_WAVES // 2)
     fixed = group_lds_bytes(0, gqa, head_dim, engine)
     per_wave = group_lds_bytes(1, gqa, head_dim, engine) - fixed

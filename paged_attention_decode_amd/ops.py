@@ -89,6 +89,59 @@ def paged_attention_decode(q, k_cache, v_cache, block_table, seq_lens, num_split
 # The reference's public name for the same operator.
 paged_attention_decode_cuda_v4 = paged_attention_decode
 
+FP8_CACHE_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
+FP8_HEAD_DIMS = (64, 128, 256)
+
+
+def paged_attention_decode_fp8(q, k_cache, v_cache, block_table, seq_lens, k_scale=1.0, v_scale=1.0,
+                               num_splits=None, scale=None):
+    """Decode over fp8 K/V caches: the same operator with half the cache bytes.
+
+    ``k_cache`` / ``v_cache`` are ``torch.float8_e4m3fn`` or
+    ``torch.float8_e5m2`` (both the same), laid out as the fp16 caches
+    ``[num_pages, page_size, num_kv_heads, head_dim]``, and hold
+    ``K / k_scale`` and ``V / v_scale`` (per-tensor scales, Python floats).
+    The result equals the fp16 operator on the dequantised caches
+    ``k_cache.float() * k_scale`` and ``v_cache.float() * v_scale``: every fp8
+    code widens to fp16 exactly.  q and the output are fp16; head_dim 64, 128
+    or 256; the MFMA engine only.  No counterpart in the reference, whose
+    caches are fp16 only (src/kernel_cuda_v4.py:37-48).
+    """
+    assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "paged_attention_decode requires GPU tensors"
+    assert block_table.is_cuda and seq_lens.is_cuda, "block_table and seq_lens must be GPU tensors"
+    assert q.dtype == torch.float16, "q must be fp16"
+    assert k_cache.dtype in FP8_CACHE_DTYPES and v_cache.dtype == k_cache.dtype, (
+        "k_cache and v_cache must both be float8_e4m3fn or both float8_e5m2"
+    )
+    assert q.dim() == 3 and k_cache.dim() == 4 and v_cache.shape == k_cache.shape, "bad q / cache shapes"
+    batch, num_q_heads, head_dim = q.shape
+    num_kv_heads = k_cache.shape[2]
+    assert k_cache.shape[3] == head_dim, "q head_dim must match the KV cache head_dim"
+    assert num_kv_heads > 0 and num_q_heads % num_kv_heads == 0, (
+        "num_q_heads must be divisible by num_kv_heads (GQA)"
+    )
+    assert num_q_heads // num_kv_heads <= MAX_GQA, f"GQA group larger than {MAX_GQA}"
+    assert head_dim in FP8_HEAD_DIMS, f"fp8 caches: head_dim must be one of {FP8_HEAD_DIMS}"
+    assert block_table.dim() == 2 and block_table.shape[0] == batch, "block_table must be [batch, max_pages]"
+    assert seq_lens.dim() == 1 and seq_lens.shape[0] == batch, "seq_lens must be [batch]"
+    assert k_cache.stride(3) == 1 and v_cache.stride(3) == 1, "K/V caches need a contiguous head_dim"
+    k_scale, v_scale = float(k_scale), float(v_scale)
+    assert k_scale > 0 and v_scale > 0 and math.isfinite(k_scale) and math.isfinite(v_scale), (
+        "k_scale and v_scale must be finite and positive"
+    )
+    if num_splits is None:
+        num_splits = 0
+    else:
+        num_splits = int(num_splits)
+        assert num_splits >= 1, "num_splits must be >= 1"
+    if block_table.dtype != torch.int32:
+        block_table = block_table.to(torch.int32)
+    if seq_lens.dtype != torch.int32:
+        seq_lens = seq_lens.to(torch.int32)
+    scale = float(scale) if scale is not None else 1.0 / math.sqrt(head_dim)
+    return ext().forward_kv8(_aligned_q(q), k_cache, v_cache, block_table, seq_lens, scale, k_scale, v_scale,
+                             num_splits)
+
 
 def paged_kv_indices(block_table, seq_lens, page_size: int):
     """Dense ``block_table [B, max_pages]`` + ``seq_lens [B]`` -> CSR ``(indptr, indices, last_page_len)``.

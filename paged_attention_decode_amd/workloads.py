@@ -17,6 +17,11 @@ and within sequences; unused block_table columns point at valid pages):
 ``algorithmic_bytes`` is the byte count the roofline uses: K and V of every
 valid token, the q read and the output write, the block_table entries of the
 used pages and seq_lens (the split workspace is excluded as overhead).
+
+``to_fp8`` turns a workload's caches into fp8 codes (float8_e4m3fn or
+float8_e5m2) of K / k_scale and V / v_scale, per-tensor scales chosen so the
+largest magnitude lands at 7/8 of the format's range; its algorithmic bytes
+count one byte per K/V element.
 """
 
 from __future__ import annotations
@@ -39,6 +44,8 @@ class Workload:
     seq_lens: torch.Tensor
     seq_lens_host: list = field(default_factory=list)
     scale: float = 0.0
+    k_scale: float = 1.0  # fp8 caches: they hold K / k_scale and V / v_scale
+    v_scale: float = 1.0
 
     @property
     def batch(self) -> int:
@@ -55,10 +62,10 @@ class Workload:
         return self.q, self.k_cache, self.v_cache, self.block_table, self.seq_lens
 
 
-def algorithmic_bytes(seq_lens, num_q_heads, num_kv_heads, head_dim, page_size) -> int:
+def algorithmic_bytes(seq_lens, num_q_heads, num_kv_heads, head_dim, page_size, kv_elem_bytes=2) -> int:
     """K+V of valid tokens + q read + out write + used block_table entries + seq_lens."""
     lens = [int(x) for x in seq_lens]
-    kv = sum(lens) * num_kv_heads * head_dim * 2 * 2
+    kv = sum(lens) * num_kv_heads * head_dim * kv_elem_bytes * 2
     qo = 2 * len(lens) * num_q_heads * head_dim * 2
     bt = sum(-(-n // page_size) for n in lens) * 4
     return kv + qo + bt + 4 * len(lens)
@@ -126,9 +133,32 @@ def make(name: str, batch: int | None = None, seed: int = 0, device: str = "cuda
 
 def bytes_of(w: Workload) -> int:
     s = w.shape
-    return algorithmic_bytes(w.seq_lens_host, s["num_q_heads"], s["num_kv_heads"], s["head_dim"], s["page_size"])
+    return algorithmic_bytes(w.seq_lens_host, s["num_q_heads"], s["num_kv_heads"], s["head_dim"], s["page_size"],
+                             w.k_cache.element_size())
 
 
 def flops_of(w: Workload) -> int:
     s = w.shape
     return algorithmic_flops(w.seq_lens_host, s["num_q_heads"], s["head_dim"])
+
+
+FP8_MAX = {torch.float8_e4m3fn: 448.0, torch.float8_e5m2: 57344.0}
+FP8_NAMES = {"e4m3fn": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+
+
+def to_fp8(w: Workload, dtype=torch.float8_e4m3fn) -> Workload:
+    """The same workload with fp8 caches (codes of K / k_scale, V / v_scale)."""
+
+    def quant(x):
+        scale = float(x.abs().max()) / (0.875 * FP8_MAX[dtype]) or 1.0
+        out = torch.empty(x.shape, dtype=dtype, device=x.device)
+        flat_in, flat_out = x.view(x.shape[0], -1), out.view(x.shape[0], -1)
+        step = max(1, (1 << 26) // max(flat_in.shape[1], 1))  # bounded fp32 temporaries
+        for i in range(0, x.shape[0], step):
+            flat_out[i:i + step] = (flat_in[i:i + step].float() / scale).to(dtype)
+        return out, scale
+
+    k8, ks = quant(w.k_cache)
+    v8, vs = quant(w.v_cache)
+    name = w.name + "_" + next(n for n, t in FP8_NAMES.items() if t == dtype)
+    return Workload(name, w.q, k8, v8, w.block_table, w.seq_lens, list(w.seq_lens_host), w.scale, ks, vs)

@@ -72,3 +72,23 @@ def test_per_config_cpu_baseline_is_on_by_default():
     finally:
         sys.argv = argv
     assert set(args.cpu_configs.split(",")) >= {"C1", "C3", "C4"}
+
+
+def test_fp8_workload_conversion():
+    # to_fp8 keeps the inputs, stores K / k_scale and V / v_scale as fp8 codes
+    # that span the format's range, and counts one byte per K/V element.
+    import torch
+
+    w = wl.make("C2", batch=2, seed=3, device="cpu")
+    for name, dt in wl.FP8_NAMES.items():
+        w8 = wl.to_fp8(w, dt)
+        assert w8.k_cache.dtype == dt and w8.v_cache.dtype == dt and w8.name.endswith(name)
+        assert w8.q is w.q and w8.block_table is w.block_table
+        top = float(w8.k_cache.float().abs().max())
+        assert abs(top - 0.875 * wl.FP8_MAX[dt]) <= 0.07 * wl.FP8_MAX[dt]
+        deq = w8.k_cache.float() * w8.k_scale
+        rel = 2.0 ** -3 if name == "e4m3fn" else 2.0 ** -2  # half an ulp of a 3- / 2-bit mantissa
+        big = w.k_cache.float().abs() > 0.1
+        assert torch.all((deq - w.k_cache.float()).abs()[big] <= rel / 2 * w.k_cache.float().abs()[big] + 1e-6)
+        kv16 = 2 * 4096 * 2 * 128 * 2 * 2  # batch x seq x kv heads x head_dim x fp16 x (K, V)
+        assert wl.bytes_of(w) - wl.bytes_of(w8) == kv16 // 2

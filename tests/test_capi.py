@@ -51,13 +51,13 @@ def test_library_exports_every_declared_symbol():
     lib = _native.capi()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.pad_decode_abi_version() == 4
+    assert lib.pad_decode_abi_version() == 5
 
 
 def test_status_strings():
     lib = _native.capi()
     assert lib.pad_status_string(0) == b"ok"
-    for code in range(1, 12):
+    for code in range(1, 13):
         assert lib.pad_status_string(code) not in (b"ok", b"unknown status")
     assert lib.pad_status_string(999) == b"unknown status"
 
@@ -191,6 +191,23 @@ def test_launch_rejects_zero_num_pages_on_the_host():
                                  None) == 2
     assert lib.pad_decode_launch_csr(fake, fake, fake, fake, fake, fake, fake, None, 0, None, 0, ctypes.byref(dm),
                                      0.1, 1, 0, None) == 2
+
+
+def test_launch_kv8_checks_format_and_scales_on_the_host():
+    # Format, head_dim and scale problems of the fp8 entry are answered
+    # before any device call.
+    lib = _native.capi()
+    fake = ctypes.c_void_p(256)
+    dm = _dims(batch=2, max_pages=4)
+    args = (fake, fake, fake, fake, fake, fake, None, 0, None, 0, ctypes.byref(dm), 0.1)
+    assert lib.pad_decode_launch_kv8(*args, 0, 1.0, 1.0, 1, None) == 12  # PAD_KV_FP16
+    assert lib.pad_decode_launch_kv8(*args, 3, 1.0, 1.0, 1, None) == 12
+    assert lib.pad_decode_launch_kv8(*args, -1, 1.0, 1.0, 1, None) == 12
+    for ks, vs in ((0.0, 1.0), (1.0, -2.0), (float("nan"), 1.0), (1.0, float("inf")), (1e31, 1.0)):
+        assert lib.pad_decode_launch_kv8(*args, 1, ks, vs, 1, None) == 12, (ks, vs)
+    dm96 = _dims(batch=2, max_pages=4, d=96)
+    assert lib.pad_decode_launch_kv8(fake, fake, fake, fake, fake, fake, None, 0, None, 0, ctypes.byref(dm96), 0.1,
+                                     2, 1.0, 1.0, 1, None) == 3
 
 
 @pytest.mark.parametrize("d", [32, 64, 96, 128, 256])
@@ -423,3 +440,25 @@ def test_launch_csr_through_c_abi(splits):
     assert lib.pad_decode_launch_csr(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), indices.data_ptr(), None,
                                      last.data_ptr(), out.data_ptr(), ws.data_ptr(), wsb.value, counters.data_ptr(),
                                      counters.numel(), ctypes.byref(dm), 0.1, splits, 0, None) == 1
+
+
+def test_fp8_plan_keeps_the_scratch_of_the_fp16_plan():
+    # pad_decode_launch_kv8 plans with one byte per K/V element: the same
+    # splits, workspace and counters as pad_decode_plan (which sizes its
+    # scratch), and 8-wave workgroups only where the fp16 plan has 4 waves
+    # for 256-byte rows.
+    import random
+
+    rng = random.Random(5)
+    for _ in range(300):
+        batch, hkv = rng.choice([1, 2, 8, 16, 32, 64, 128, 300]), rng.choice([1, 2, 4, 8])
+        gqa, d = rng.choice([1, 2, 4, 6, 8, 16]), rng.choice([64, 128, 256])
+        ps = rng.choice([1, 4, 12, 16, 32, 64])
+        max_pages = rng.randint(1, 4096) // ps + 1
+        a = heuristics.plan(batch, hkv * gqa, hkv, d, ps, max_pages)
+        b = heuristics.plan(batch, hkv * gqa, hkv, d, ps, max_pages, kv_bytes=1)
+        assert (a.num_splits, a.pages_per_split, a.single_pass, a.workspace_bytes, a.counters) == (
+            b.num_splits, b.pages_per_split, b.single_pass, b.workspace_bytes, b.counters)
+        assert b.waves_per_group >= a.waves_per_group
+        if d != 128:
+            assert b.waves_per_group == a.waves_per_group

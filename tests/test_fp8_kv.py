@@ -1,0 +1,232 @@
+"""GPU tests of the decode over fp8 K/V caches (pad_decode_launch_kv8).
+
+The caches hold float8_e4m3fn or float8_e5m2 codes of K / k_scale and
+V / v_scale; q and the output are fp16.  No counterpart in the reference,
+whose caches are fp16 only (src/kernel_cuda_v4.py:37-48).
+
+* Parity: against the fp32 oracle on the dequantised caches
+  (oracle/reference.py decode_fp8_protocol), atol = rtol = 2e-3 and the
+  reference's own 1e-2 / 1e-3, over both formats, head_dim 64/128/256, page
+  sizes of the uniform, sub-page and generic block modes, split counts and
+  scales other than 1.
+* Bit-exact: with unit scales the fp8 kernel must return exactly what the
+  fp16 kernel returns on the same codes widened to fp16 by PyTorch (same
+  plan, same split count), on random data and on caches that hold every
+  finite code of the format: every fp8 value is an fp16 value, and the
+  kernel's in-register conversion must produce it.
+* NaN codes in unused pages and in the unused slots of a last page leave the
+  output untouched; error statuses for a bad format, head_dim and scale.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import pytest
+import torch
+
+from oracle.reference import decode_fp8_protocol
+from paged_attention_decode_amd import _native
+from tests.helpers import assert_parity, make_cache, shuffled_table
+
+pytestmark = pytest.mark.gpu
+
+FMTS = {"e4m3fn": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+# Largest finite magnitude of each format.
+FMAX = {"e4m3fn": 448.0, "e5m2": 57344.0}
+
+
+def _quant(x, fmt, scale):
+    """x / scale as fp8 codes (x / scale stays inside the format's range)."""
+    y = x / scale
+    assert float(y.abs().max()) < FMAX[fmt]
+    return y.to(FMTS[fmt])
+
+
+def _case(lens, ps, hkv, gqa, d, seed, spare=2, extra=1):
+    bt, n = shuffled_table(lens, ps, spare_pages=spare, extra_cols=extra, seed=seed)
+    k, v = make_cache(n, ps, hkv, d, seed=seed)
+    q = torch.randn(len(lens), hkv * gqa, d, generator=torch.Generator().manual_seed(seed))
+    return q, k, v, bt, torch.tensor(lens, dtype=torch.int32)
+
+
+def _fp8(q, k8, v8, bt, sl, ks, vs, splits):
+    import paged_attention_decode_amd as pad
+
+    out = pad.paged_attention_decode_fp8(q.half().cuda(), k8.cuda(), v8.cuda(), bt.cuda(), sl.cuda(),
+                                         k_scale=ks, v_scale=vs, num_splits=splits)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16 and out.shape == q.shape
+    return out.cpu()
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("ps", [16, 1, 4, 12, 64])
+def test_fp8_matches_oracle(fmt, d, ps):
+    lens = [1, ps + 3, 150, 777]
+    q, k, v, bt, sl = _case(lens, ps, 2, 6, d, seed=ps + d)
+    # Scales that are not powers of two, with the codes spanning the range.
+    ks, vs = float(k.abs().max()) / 300.0, float(v.abs().max()) / 111.0
+    k8, v8 = _quant(k, fmt, ks), _quant(v, fmt, vs)
+    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs)
+    for splits in (None, 1, 5):
+        assert_parity(_fp8(q, k8, v8, bt, sl, ks, vs, splits), expected)
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("hkv,gqa", [(1, 1), (4, 2), (2, 8), (1, 16)])
+def test_fp8_group_sizes(fmt, hkv, gqa):
+    lens = [33, 2000, 5]
+    q, k, v, bt, sl = _case(lens, 16, hkv, gqa, 128, seed=hkv * 31 + gqa)
+    ks, vs = 0.02, 0.5
+    k8, v8 = _quant(k, fmt, ks), _quant(v, fmt, vs)
+    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs)
+    for splits in (None, 64):
+        assert_parity(_fp8(q, k8, v8, bt, sl, ks, vs, splits), expected)
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_unit_scales_equal_the_fp16_kernel_bitwise(fmt, d):
+    import paged_attention_decode_amd as pad
+
+    lens = [7, 300, 1500, 64]
+    q, k, v, bt, sl = _case(lens, 16, 2, 4, d, seed=d + 1)
+    k8, v8 = k.to(FMTS[fmt]), v.to(FMTS[fmt])
+    qd, btd, sld = q.half().cuda(), bt.cuda(), sl.cuda()
+    for splits in (None, 1, 8):
+        a = pad.paged_attention_decode_fp8(qd, k8.cuda(), v8.cuda(), btd, sld, num_splits=splits)
+        b = pad.paged_attention_decode(qd, k8.half().cuda(), v8.half().cuda(), btd, sld, num_splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), (splits, (a.float() - b.float()).abs().max().item())
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_every_finite_code_converts_exactly(fmt):
+    # K and V cycle through every finite code (subnormals, extremes, both
+    # zeros) in every head_dim position; unit scales, so the fp8 kernel must
+    # match the fp16 kernel on PyTorch's widening of the same codes.
+    import paged_attention_decode_amd as pad
+
+    dt = FMTS[fmt]
+    codes = torch.arange(256, dtype=torch.uint8)
+    finite = codes[torch.isfinite(codes.view(dt).float())]
+    ps, hkv, d, n_pages = 16, 1, 128, 8
+    n = n_pages * ps * hkv * d
+    idx = torch.arange(n)
+    kc = finite[(idx * 7) % finite.numel()].view(n_pages, ps, hkv, d)
+    vc = finite[(idx * 11 + 3) % finite.numel()].view(n_pages, ps, hkv, d)
+    k8, v8 = kc.view(dt), vc.view(dt)
+    # Small q keeps the scores of the largest e5m2 codes finite in fp16 terms.
+    q = torch.randn(2, 4, d, generator=torch.Generator().manual_seed(0)) * (1e-4 if fmt == "e5m2" else 1e-2)
+    bt = torch.arange(n_pages, dtype=torch.int32).view(2, n_pages // 2)
+    sl = torch.tensor([n_pages // 2 * ps, n_pages // 2 * ps - 5], dtype=torch.int32)
+    qd, btd, sld = q.half().cuda(), bt.cuda(), sl.cuda()
+    for splits in (None, 1, 4):
+        a = pad.paged_attention_decode_fp8(qd, k8.cuda(), v8.cuda(), btd, sld, num_splits=splits)
+        b = pad.paged_attention_decode(qd, k8.half().cuda(), v8.half().cuda(), btd, sld, num_splits=splits)
+        torch.cuda.synchronize()
+        assert torch.isfinite(b).all()
+        assert torch.equal(a, b), (splits, (a.float() - b.float()).abs().max().item())
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_nan_codes_in_unused_slots(fmt):
+    # Unused pages and the unused tail of each last page hold NaN codes (and
+    # infinities for e5m2): a kernel that reads them into the result gives NaN.
+    lens = [37, 5]
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=9, spare=3, extra=2)
+    ks, vs = 0.05, 0.05
+    k8, v8 = _quant(k, fmt, ks), _quant(v, fmt, vs)
+    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs)
+    ku, vu = k8.view(torch.uint8).clone(), v8.view(torch.uint8).clone()
+    bad = [0x7F, 0xFF] if fmt == "e4m3fn" else [0x7F, 0xFE, 0x7C, 0xFC]
+    used = {int(bt[0, j]) for j in range(3)} | {int(bt[1, 0])}
+    for p in range(ku.shape[0]):
+        if p not in used:
+            ku[p] = bad[p % len(bad)]
+            vu[p] = bad[(p + 1) % len(bad)]
+    for last in (int(bt[0, 2]), int(bt[1, 0])):
+        ku[last, 5:] = bad[0]
+        vu[last, 5:] = bad[-1]
+    k8p, v8p = ku.view(FMTS[fmt]), vu.view(FMTS[fmt])
+    for s in (None, 1, 2):
+        out = _fp8(q, k8p, v8p, bt, sl, ks, vs, s)
+        assert torch.isfinite(out).all()
+        assert_parity(out, expected)
+
+
+def test_nan_code_in_a_used_slot_propagates():
+    # A NaN code inside the sequence is a NaN key: its query rows become NaN,
+    # as the fp16 kernel and the oracle give for a NaN in an fp16 cache.
+    lens = [40]
+    q, k, v, bt, sl = _case(lens, 16, 1, 2, 64, seed=5, spare=0, extra=0)
+    k8 = _quant(k, "e4m3fn", 0.02)
+    ku = k8.view(torch.uint8).clone()
+    ku[int(bt[0, 1]), 3, 0, 10] = 0x7F
+    out = _fp8(q, ku.view(torch.float8_e4m3fn), _quant(v, "e4m3fn", 0.02), bt, sl, 0.02, 0.02, None)
+    assert torch.isnan(out).all()
+
+
+def test_kv8_through_the_c_abi():
+    lib = _native.capi()
+    lens = [1, 77, 400, 1000]
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=3)
+    ks, vs = float(k.abs().max()) / 400.0, float(v.abs().max()) / 50.0
+    k8, v8 = _quant(k, "e4m3fn", ks), _quant(v, "e4m3fn", vs)
+    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs)
+    qd, kd, vd, btd, sld = q.half().cuda(), k8.cuda(), v8.cuda(), bt.cuda(), sl.cuda()
+    out = torch.empty_like(qd)
+    dm = _native.dims_for(qd, kd, vd, btd, sld, out)
+    for splits in (0, 1, 6):
+        wsb, nc = ctypes.c_size_t(), ctypes.c_int64()
+        assert lib.pad_decode_workspace_bytes(ctypes.byref(dm), splits, 0, ctypes.byref(wsb)) == 0
+        assert lib.pad_decode_counters_needed(ctypes.byref(dm), splits, 0, ctypes.byref(nc)) == 0
+        ws = torch.empty(max(wsb.value, 1), dtype=torch.uint8, device="cuda")
+        counters = torch.zeros(max(nc.value, 1), dtype=torch.int32, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+        out.fill_(float("nan"))
+        st = lib.pad_decode_launch_kv8(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), btd.data_ptr(), sld.data_ptr(),
+                                       out.data_ptr(), ws.data_ptr(), ws.numel(), counters.data_ptr(),
+                                       counters.numel(), ctypes.byref(dm), 1.0 / math.sqrt(128), 1, ks, vs, splits,
+                                       stream)
+        assert st == 0, lib.pad_status_string(st)
+        torch.cuda.synchronize()
+        assert_parity(out, expected)
+        assert torch.all(counters == 0)
+
+
+def test_fp8_rejects_bad_arguments():
+    import paged_attention_decode_amd as pad
+
+    q, k, v, bt, sl = _case([20], 16, 2, 2, 96, seed=1)
+    k8 = k.to(torch.float8_e4m3fn).cuda()
+    with pytest.raises(AssertionError, match="head_dim"):
+        pad.paged_attention_decode_fp8(q.half().cuda(), k8, k8, bt.cuda(), sl.cuda())
+    q, k, v, bt, sl = _case([20], 16, 2, 2, 64, seed=1)
+    qd, btd, sld = q.half().cuda(), bt.cuda(), sl.cuda()
+    k8, v5 = k.to(torch.float8_e4m3fn).cuda(), v.to(torch.float8_e5m2).cuda()
+    with pytest.raises(AssertionError, match="float8"):
+        pad.paged_attention_decode_fp8(qd, k8, v5, btd, sld)
+    for bad in (0.0, -1.0, float("inf"), float("nan")):
+        with pytest.raises(AssertionError, match="k_scale"):
+            pad.paged_attention_decode_fp8(qd, k8, k8, btd, sld, k_scale=bad)
+    # The binding and the C ABI refuse them as well.
+    from paged_attention_decode_amd._native import ext
+
+    with pytest.raises(RuntimeError, match="fp8"):
+        ext().forward_kv8(qd, k8, k8, btd, sld, 0.125, -1.0, 1.0, 0)
+    with pytest.raises(RuntimeError, match="float8"):
+        ext().forward_kv8(qd, k8.half(), k8.half(), btd, sld, 0.125, 1.0, 1.0, 0)
+    lib = _native.capi()
+    out = torch.empty_like(qd)
+    dm = _native.dims_for(qd, k8, k8, btd, sld, out)
+    args = (qd.data_ptr(), k8.data_ptr(), k8.data_ptr(), btd.data_ptr(), sld.data_ptr(), out.data_ptr(), None, 0,
+            None, 0, ctypes.byref(dm), 0.125)
+    assert lib.pad_decode_launch_kv8(*args, 0, 1.0, 1.0, 1, None) == 12  # fp16 is pad_decode_launch's
+    assert lib.pad_decode_launch_kv8(*args, 3, 1.0, 1.0, 1, None) == 12
+    assert lib.pad_decode_launch_kv8(*args, 1, 0.0, 1.0, 1, None) == 12
+    assert lib.pad_decode_launch_kv8(*args, 2, 1.0, float("nan"), 1, None) == 12
+    torch.cuda.synchronize()

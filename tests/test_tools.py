@@ -52,7 +52,7 @@ def test_profile_summary_on_synthetic_runs(tmp_path):
     from paged_attention_decode_amd import profile_summary as ps
 
     root = str(tmp_path)
-    kname = "void pad::pad_phase1_kernel<128, 1, 0, 0>(pad::Phase1Args)"
+    kname = "void pad::pad_phase1_kernel<128, 1, 0, 0, 0>(pad::Phase1Args)"
     log = "x: 4 calls over 3 input set(s); algorithmic bytes/call 1000000 (first set), 1200000 (mean over the calls)\n"
     for run in ("trace_T", "pmc_FETCH_SIZE_T", "pmc_WRITE_SIZE_T", "pmc_REQ_T"):
         open(f"{root}/{run}.log", "w").write(log)
