@@ -92,6 +92,10 @@ def _counter(root, run, ctr):
     k = [float(r["Counter_Value"]) for r in rs if KERNEL in r["Kernel_Name"] and r["Counter_Name"] == ctr]
     c = [float(r["Counter_Value"]) for r in rs
          if "copyBuffer" in r["Kernel_Name"] and r["Grid_Size"] == COPY_GRID and r["Counter_Name"] == ctr]
+    # Every copy dispatch counted must be the calibration copy of known size.
+    if c and max(c) > 1.01 * min(c):
+        raise ValueError(f"{run}: copy dispatches of grid {COPY_GRID} with different {ctr} ({min(c)} .. {max(c)}): "
+                         "some are not the calibration copy")
     return (statistics.median(k) if k else None), (statistics.median(c) if c else None), len(k)
 
 

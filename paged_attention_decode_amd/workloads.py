@@ -155,7 +155,9 @@ def to_fp8(w: Workload, dtype=torch.float8_e4m3fn) -> Workload:
         flat_in, flat_out = x.view(x.shape[0], -1), out.view(x.shape[0], -1)
         step = max(1, (1 << 26) // max(flat_in.shape[1], 1))  # bounded fp32 temporaries
         for i in range(0, x.shape[0], step):
-            flat_out[i:i + step] = (flat_in[i:i + step].float() / scale).to(dtype)
+            # copy_ with a dtype change is an elementwise cast, never a device
+            # memcpy (a profile's copy-kernel calibration counts those).
+            flat_out[i:i + step].copy_(flat_in[i:i + step].float().div_(scale))
         return out, scale
 
     k8, ks = quant(w.k_cache)
