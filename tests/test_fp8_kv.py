@@ -230,3 +230,38 @@ def test_fp8_rejects_bad_arguments():
     assert lib.pad_decode_launch_kv8(*args, 1, 0.0, 1.0, 1, None) == 12
     assert lib.pad_decode_launch_kv8(*args, 2, 1.0, float("nan"), 1, None) == 12
     torch.cuda.synchronize()
+
+
+def test_fp8_graph_capture_replays():
+    # The fp8 entry under HIP graph capture: scratch exists before capture,
+    # every replay with new q written in place equals an eager call.
+    import paged_attention_decode_amd as pad
+
+    lens = [4096, 300, 2500, 1]
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=93)
+    ks, vs = float(k.abs().max()) / 300.0, float(v.abs().max()) / 111.0
+    k8, v8 = _quant(k, "e4m3fn", ks), _quant(v, "e4m3fn", vs)
+    dev = [k8.cuda(), v8.cuda(), bt.cuda(), sl.cuda()]
+    qs = [torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(94 + i)).half().cuda()
+          for i in range(3)]
+    q_static = qs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            pad.paged_attention_decode_fp8(q_static, *dev, k_scale=ks, v_scale=vs)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out_static = pad.paged_attention_decode_fp8(q_static, *dev, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    for rep in range(2):
+        for qn in qs:
+            q_static.copy_(qn)
+            graph.replay()
+            torch.cuda.synchronize()
+            eager = pad.paged_attention_decode_fp8(qn, *dev, k_scale=ks, v_scale=vs)
+            torch.cuda.synchronize()
+            assert torch.equal(out_static, eager), f"replay {rep} differs from the eager call"
+    assert_parity(out_static.cpu(), decode_fp8_protocol(qs[-1].float().cpu(), k8, v8, bt, sl, ks, vs))
