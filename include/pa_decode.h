@@ -224,8 +224,10 @@ int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache,
  * head_dim 64, 128 or 256.  Each element is widened to fp16 exactly in
  * registers, so the result equals the fp16 path's on the dequantized
  * caches up to fp32 rounding: k_scale goes into the softmax scale and
- * v_scale into the output normalisation.  Same plan, workspace and
- * counters as pad_decode_launch() (pad_decode_plan()).  No counterpart in
+ * v_scale into the output normalisation.  Same splits, workspace and
+ * counters as pad_decode_launch() (pad_decode_plan(),
+ * pad_decode_workspace_bytes(), pad_decode_counters_needed()); workgroups
+ * may have more waves, as the rows are half the bytes.  No counterpart in
  * the reference, whose caches are fp16 only (src/kernel_cuda_v4.py:37-48);
  * it is the next data format of the same operator. */
 int pad_decode_launch_kv8(const void* q, const void* k_cache,
