@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define PAD_ABI_VERSION 5
+#define PAD_ABI_VERSION 6
 
 /* Largest supported GQA group (query heads per KV head); the reference's
  * bound is the same (cuda/kernel_v4_split_k.cu:44). */
@@ -324,6 +324,57 @@ int pad_decode_launch_worklist_csr(const void* q, const void* k_cache,
                                    const pad_decode_dims* dims, float scale,
                                    int num_splits, const void* worklist,
                                    size_t worklist_bytes, void* stream);
+
+/* Every option of one decode launch in one descriptor, for callers that
+ * need a combination the entry points above do not offer (fp8 caches with a
+ * CSR page index or a work list).  Fields:
+ *   block_table / seq_lens: the dense page index; with a CSR index
+ *     (indptr != NULL) block_table is `indices`, seq_lens is unused and
+ *     dims->max_pages is the number of entries of `indices`, as for
+ *     pad_decode_launch_csr();
+ *   worklist / worklist_bytes: optional, a list planned for the same call
+ *     (pad_decode_plan_worklist_call()); NULL plans in the kernel;
+ *   engine: 0 (MFMA) or 1 (VALU: fp16 caches, no work list;
+ *     PAD_ERR_INVALID_SHAPE otherwise, PAD_ERR_KV_FORMAT with fp8);
+ *   kv_format, k_scale, v_scale: as pad_decode_launch_kv8(); the scales are
+ *     ignored for PAD_KV_FP16.
+ * pad_decode_launch_call() runs exactly what the matching entry point runs:
+ * pad_decode_launch_ex (no events), _csr, _worklist, _worklist_csr or _kv8,
+ * with the same workspace and counters.  No counterpart in the reference. */
+typedef struct pad_decode_call {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const int32_t* block_table;
+  const int32_t* seq_lens;
+  const int32_t* indptr;          /* CSR [batch + 1], or NULL             */
+  const int32_t* last_page_len;   /* CSR [batch], or NULL                 */
+  void* out;
+  void* workspace;
+  size_t workspace_bytes;
+  int32_t* counters;
+  int64_t num_counters;
+  const void* worklist;
+  size_t worklist_bytes;
+  float scale;
+  int32_t num_splits;
+  int32_t engine;
+  int32_t kv_format;
+  float k_scale;
+  float v_scale;
+} pad_decode_call;
+
+int pad_decode_launch_call(const pad_decode_call* call,
+                           const pad_decode_dims* dims, void* stream);
+
+/* The work list of the launch `call` describes (its index fields, engine
+ * and kv_format; the data pointers are not read), written to `worklist`
+ * (pad_decode_worklist_bytes() bytes, csr = indptr != NULL).  A list
+ * planned for another kv_format is ignored by the launch, which then plans
+ * in the kernel: fp8 launches may run workgroups of more waves. */
+int pad_decode_plan_worklist_call(const pad_decode_call* call,
+                                  const pad_decode_dims* dims, void* worklist,
+                                  size_t worklist_bytes, void* stream);
 
 /* Compute units of the current device (cached per device). */
 int pad_device_num_cus(int* num_cus);

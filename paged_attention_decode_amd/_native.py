@@ -5,8 +5,8 @@
   against PyTorch's HIP runtime).
 * ``capi()`` - ``libpa_decode.so`` opened with ctypes, with argument types
   for every entry point of include/pa_decode.h, plus the ``PadDims`` /
-  ``PadPlan`` structures that mirror ``pad_decode_dims`` /
-  ``pad_decode_plan_t``.
+  ``PadPlan`` / ``PadCall`` structures that mirror ``pad_decode_dims`` /
+  ``pad_decode_plan_t`` / ``pad_decode_call``.
 * ``probe()`` - ``libpa_probe.so``, the bandwidth probes used by
   ``roofline.py`` (measurement tooling, not the decode path).
 * ``timeline()`` - ``libpa_decode_tl.so``, the decode library built with
@@ -83,6 +83,33 @@ class PadPlan(ctypes.Structure):
     ]
 
 
+class PadCall(ctypes.Structure):
+    """Mirror of ``pad_decode_call`` (include/pa_decode.h)."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k_cache", ctypes.c_void_p),
+        ("v_cache", ctypes.c_void_p),
+        ("block_table", ctypes.c_void_p),
+        ("seq_lens", ctypes.c_void_p),
+        ("indptr", ctypes.c_void_p),
+        ("last_page_len", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("counters", ctypes.c_void_p),
+        ("num_counters", ctypes.c_int64),
+        ("worklist", ctypes.c_void_p),
+        ("worklist_bytes", ctypes.c_size_t),
+        ("scale", ctypes.c_float),
+        ("num_splits", ctypes.c_int32),
+        ("engine", ctypes.c_int32),
+        ("kv_format", ctypes.c_int32),
+        ("k_scale", ctypes.c_float),
+        ("v_scale", ctypes.c_float),
+    ]
+
+
 # Exported entry points and their C signatures (argtypes, restype).
 _VP = ctypes.c_void_p
 SIGNATURES = {
@@ -138,6 +165,9 @@ SIGNATURES = {
          ctypes.c_float, ctypes.c_int, _VP, ctypes.c_size_t, _VP],
         ctypes.c_int,
     ),
+    "pad_decode_launch_call": ([ctypes.POINTER(PadCall), ctypes.POINTER(PadDims), _VP], ctypes.c_int),
+    "pad_decode_plan_worklist_call": (
+        [ctypes.POINTER(PadCall), ctypes.POINTER(PadDims), _VP, ctypes.c_size_t, _VP], ctypes.c_int),
     "pad_device_num_cus": ([ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
     "pad_status_string": ([ctypes.c_int], ctypes.c_char_p),
     "pad_decode_abi_version": ([], ctypes.c_int),

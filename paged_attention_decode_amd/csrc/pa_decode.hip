@@ -2043,6 +2043,17 @@ static size_t worklist_bytes_for(const pad_decode_plan_t& plan, const pad_decode
   return sizeof(int32_t) * (size_t)(kWlHeaderInts + kWlRecordInts * G);
 }
 
+// fp8 caches: a known format, the MFMA engine, head_dim 64/128/256 and
+// finite positive scales (the scales are not read for fp16).
+static int check_kv_format(int kv_format, int engine, const pad_decode_dims* d, float k_scale, float v_scale) {
+  if (kv_format == PAD_KV_FP16) return PAD_OK;
+  if (kv_format != PAD_KV_FP8_E4M3FN && kv_format != PAD_KV_FP8_E5M2) return PAD_ERR_KV_FORMAT;
+  if (engine != 0) return PAD_ERR_KV_FORMAT;
+  if (d && d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return PAD_ERR_UNSUPPORTED_HEAD_DIM;
+  if (!(k_scale > 0.0f) || !(v_scale > 0.0f) || k_scale > 1.0e30f || v_scale > 1.0e30f) return PAD_ERR_KV_FORMAT;
+  return PAD_OK;
+}
+
 // kv_format: PAD_KV_FP16, or an fp8 format with per-tensor scales k_scale,
 // v_scale (the caches hold K / k_scale and V / v_scale).
 static int launch_impl(const void* q, const void* k, const void* v, const int32_t* bt, const int32_t* sl,
@@ -2051,15 +2062,11 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
                        int num_splits, int engine, void* const* events, void* stream,
                        const void* worklist = nullptr, size_t worklist_bytes = 0, int kv_format = PAD_KV_FP16,
                        float k_scale = 1.0f, float v_scale = 1.0f) {
-  if (kv_format != PAD_KV_FP16) {
-    if (kv_format != PAD_KV_FP8_E4M3FN && kv_format != PAD_KV_FP8_E5M2) return PAD_ERR_KV_FORMAT;
-    if (engine != 0) return PAD_ERR_KV_FORMAT;
-    if (d && d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return PAD_ERR_UNSUPPORTED_HEAD_DIM;
-    if (!(k_scale > 0.0f) || !(v_scale > 0.0f) || k_scale > 1.0e30f || v_scale > 1.0e30f) return PAD_ERR_KV_FORMAT;
-  }
+  int st = check_kv_format(kv_format, engine, d, k_scale, v_scale);
+  if (st != PAD_OK) return st;
   Launch L;
-  int st = setup_launch(q, k, v, bt, sl, indptr, lpl, out, ws, ws_bytes, counters, num_counters, d, scale,
-                        num_splits, engine, true, &L, kv_format == PAD_KV_FP16 ? 2 : 1);
+  st = setup_launch(q, k, v, bt, sl, indptr, lpl, out, ws, ws_bytes, counters, num_counters, d, scale,
+                    num_splits, engine, true, &L, kv_format == PAD_KV_FP16 ? 2 : 1);
   if (st != PAD_OK || L.empty) return st;
   if (kv_format != PAD_KV_FP16) {
     // The caches hold K / k_scale and V / v_scale: k_scale multiplies every
@@ -2099,12 +2106,14 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
 
 // Writes the work list of a launch with these dims and indices (one wave per
 // workgroup slot of the decode grid).
+// kv_bytes: bytes per K/V element of the launch the list is for (the wave
+// count, and so the list's plan key, depends on it).
 static int plan_worklist_impl(const int32_t* bt, const int32_t* sl, const int32_t* indptr, const int32_t* lpl,
                               const pad_decode_dims* d, int num_splits, void* worklist, size_t worklist_bytes,
-                              void* stream) {
+                              void* stream, int kv_bytes = 2) {
   Launch L;
   int st = setup_launch(nullptr, nullptr, nullptr, bt, sl, indptr, lpl, nullptr, nullptr, 0, nullptr, 0, d, 1.0f,
-                        num_splits, 0, false, &L);
+                        num_splits, 0, false, &L, kv_bytes);
   if (st != PAD_OK) return st;
   if (!worklist) return PAD_ERR_NULL_POINTER;
   if (worklist_bytes < worklist_bytes_for(L.plan, d)) return PAD_ERR_WORKSPACE;
@@ -2294,6 +2303,30 @@ int pad_decode_launch_worklist_csr(const void* q, const void* k_cache, const voi
   return pad::launch_impl(q, k_cache, v_cache, indices, nullptr, indptr, last_page_len, out, workspace,
                           workspace_bytes, counters, num_counters, dims, scale, num_splits, 0, nullptr, stream,
                           worklist, worklist_bytes);
+}
+
+int pad_decode_launch_call(const pad_decode_call* c, const pad_decode_dims* dims, void* stream) {
+  if (!c) return PAD_ERR_NULL_POINTER;
+  const bool csr = c->indptr != nullptr || c->last_page_len != nullptr;
+  if (csr && (!c->indptr || !c->last_page_len)) return PAD_ERR_NULL_POINTER;
+  if (c->worklist && c->engine != 0) return PAD_ERR_INVALID_SHAPE;  // work lists serve the MFMA engine
+  return pad::launch_impl(c->q, c->k_cache, c->v_cache, c->block_table, csr ? nullptr : c->seq_lens, c->indptr,
+                          c->last_page_len, c->out, c->workspace, c->workspace_bytes, c->counters, c->num_counters,
+                          dims, c->scale, c->num_splits, c->engine, nullptr, stream, c->worklist, c->worklist_bytes,
+                          c->kv_format, c->k_scale, c->v_scale);
+}
+
+int pad_decode_plan_worklist_call(const pad_decode_call* c, const pad_decode_dims* dims, void* worklist,
+                                  size_t worklist_bytes, void* stream) {
+  if (!c) return PAD_ERR_NULL_POINTER;
+  const bool csr = c->indptr != nullptr || c->last_page_len != nullptr;
+  if (csr && (!c->indptr || !c->last_page_len)) return PAD_ERR_NULL_POINTER;
+  if (c->engine != 0) return PAD_ERR_INVALID_SHAPE;  // work lists serve the MFMA engine
+  const int st = pad::check_kv_format(c->kv_format, 0, dims, c->k_scale, c->v_scale);
+  if (st != PAD_OK) return st;
+  return pad::plan_worklist_impl(c->block_table, csr ? nullptr : c->seq_lens, c->indptr, c->last_page_len, dims,
+                                 c->num_splits, worklist, worklist_bytes, stream,
+                                 c->kv_format == PAD_KV_FP16 ? 2 : 1);
 }
 
 int pad_decode_counters_init(int32_t* counters, int64_t num_counters, void* stream) {

@@ -5,15 +5,14 @@
 // (cuda/kernel_v4_split_k.cu:205-268).  This file holds no kernels: it reads
 // shapes, strides and data pointers from the tensors, allocates the output
 // from PyTorch's caching allocator, and calls
-// pad_decode_launch_ex() (or pad_decode_launch_csr()) on PyTorch's current HIP
-// stream of q's device, with
-// persistent split scratch (workspace + arrival counters) per (device,
-// stream).
+// pad_decode_launch_ex() (dense table), pad_decode_launch_kv8() (dense
+// table, fp8 caches) or pad_decode_launch_call() (CSR index, work lists) on
+// PyTorch's current HIP stream of q's device, with persistent split scratch
+// (workspace + arrival counters) per (device, stream).
 // plan_worklist / plan_worklist_csr and forward_worklist / forward_worklist_csr
 // split a decode into a plan (once per decode step) and runs (once per
-// layer) over pad_decode_plan_worklist / pad_decode_launch_worklist.
-// forward_kv8 decodes over fp8 (e4m3fn / e5m2) caches through
-// pad_decode_launch_kv8.
+// layer) over pad_decode_plan_worklist_call / pad_decode_launch_call.  The
+// CSR and work-list entries take fp16 or fp8 (e4m3fn / e5m2) caches.
 // Argument errors surface as RuntimeError (the reference used TORCH_CHECK,
 // cuda/kernel_v4_split_k.cu:216-223).  No host synchronisation.
 
@@ -218,22 +217,29 @@ torch::Tensor forward_kv8(torch::Tensor q, torch::Tensor k_cache, torch::Tensor 
   return out;
 }
 
-// Decode with a CSR page index: the page ids of sequence b are
-// indices[indptr[b] : indptr[b+1]] and its last page holds last_page_len[b]
-// tokens (the (indptr, indices, last_page_len) triple the reference's
-// FlashInfer adapter builds, src/flashinfer_adapter.py:40-65).
-torch::Tensor forward_csr(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor indptr,
-                          torch::Tensor indices, torch::Tensor last_page_len, double scale, int64_t num_splits,
-                          int64_t engine) {
+// PAD_KV_* format of the caches: both float16, or both the same fp8 type
+// (float8_e4m3fn / float8_e5m2); q is float16.
+int cache_format(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache) {
+  TORCH_CHECK(q.scalar_type() == at::kHalf, "pa_decode: q must be float16");
+  const at::ScalarType kt = k_cache.scalar_type();
+  TORCH_CHECK(v_cache.scalar_type() == kt, "pa_decode: k_cache and v_cache must have the same dtype");
+  if (kt == at::kHalf) return PAD_KV_FP16;
+  if (kt == at::kFloat8_e4m3fn) return PAD_KV_FP8_E4M3FN;
+  if (kt == at::kFloat8_e5m2) return PAD_KV_FP8_E5M2;
+  TORCH_CHECK(false, "pa_decode: k_cache and v_cache must be float16, float8_e4m3fn or float8_e5m2");
+  return PAD_KV_FP16;
+}
+
+// Checks of the CSR entries: q, caches and the (indptr, indices,
+// last_page_len) triple on one GPU, int32, contiguous, sized by q's batch.
+void check_csr(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache,
+               const torch::Tensor& indptr, const torch::Tensor& indices, const torch::Tensor& last_page_len) {
   TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && indptr.is_cuda() && indices.is_cuda() &&
                   last_page_len.is_cuda(),
               "pa_decode: all tensors must be on the GPU");
   TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() && q.device() == indptr.device() &&
                   q.device() == indices.device() && q.device() == last_page_len.device(),
               "pa_decode: all tensors must be on the same device");
-  TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
-                  v_cache.scalar_type() == at::kHalf,
-              "pa_decode: q, k_cache and v_cache must be float16");
   TORCH_CHECK(indptr.scalar_type() == at::kInt && indices.scalar_type() == at::kInt &&
                   last_page_len.scalar_type() == at::kInt,
               "pa_decode: indptr, indices and last_page_len must be int32");
@@ -248,36 +254,114 @@ torch::Tensor forward_csr(torch::Tensor q, torch::Tensor k_cache, torch::Tensor 
               "pa_decode: indptr, indices and last_page_len must be contiguous 1-D tensors");
   TORCH_CHECK(indices.size(0) <= INT32_MAX, "pa_decode: too many page ids");
   TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
+}
 
-  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
-  pad_decode_dims d;
-  fill_dims(q, k_cache, v_cache, indices.view({1, -1}), last_page_len, out, &d);
-  d.max_pages = static_cast<int32_t>(indices.size(0));
-  d.bt_stride[0] = 0;
-  d.bt_stride[1] = 1;
+void check_worklist(const torch::Tensor& q, const torch::Tensor& worklist) {
+  TORCH_CHECK(worklist.is_cuda() && worklist.device() == q.device() && worklist.scalar_type() == at::kByte &&
+                  worklist.is_contiguous(),
+              "pa_decode: worklist must be a contiguous uint8 tensor on q's device");
+}
 
-  const int cus = cached_cus(q.get_device());
+// The page index of one launch: dense (block_table, seq_lens) or CSR
+// (indices, indptr, last_page_len), as raw pointers.
+struct PageIndex {
+  const int32_t* ids = nullptr;  // block_table, or CSR indices
+  const int32_t* seq_lens = nullptr;
+  const int32_t* indptr = nullptr;
+  const int32_t* last_page_len = nullptr;
+};
+
+PageIndex dense_index(const torch::Tensor& block_table, const torch::Tensor& seq_lens) {
+  PageIndex ix;
+  ix.ids = block_table.data_ptr<int32_t>();
+  ix.seq_lens = seq_lens.data_ptr<int32_t>();
+  return ix;
+}
+
+PageIndex csr_index(const torch::Tensor& indptr, const torch::Tensor& indices, const torch::Tensor& last_page_len) {
+  PageIndex ix;
+  ix.ids = indices.data_ptr<int32_t>();
+  ix.indptr = indptr.data_ptr<int32_t>();
+  ix.last_page_len = last_page_len.data_ptr<int32_t>();
+  return ix;
+}
+
+// The dims of a CSR launch: fill_dims() with `indices` as a one-row table
+// whose width is the number of entries.
+void csr_dims(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache,
+              const torch::Tensor& indices, const torch::Tensor& last_page_len, const torch::Tensor& out,
+              pad_decode_dims* d) {
+  fill_dims(q, k_cache, v_cache, indices.view({1, -1}), last_page_len, out, d);
+  d->max_pages = static_cast<int32_t>(indices.size(0));
+  d->bt_stride[0] = 0;
+  d->bt_stride[1] = 1;
+}
+
+// One launch through pad_decode_launch_call() on PyTorch's current stream of
+// q's device, with that stream's split scratch sized by the dense (or CSR)
+// plan of d.  worklist may be undefined (plan in the kernel).
+torch::Tensor launch_call(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache,
+                          const torch::Tensor& out, const pad_decode_dims& d, const PageIndex& ix,
+                          const torch::Tensor& worklist, double scale, int64_t num_splits, int64_t engine,
+                          int kv_format, double k_scale, double v_scale) {
+  const bool csr = ix.indptr != nullptr;
   pad_decode_plan_t plan;
-  int st = pad_decode_plan_csr(&d, static_cast<int>(num_splits), cus, &plan);
+  const int cus = cached_cus(q.get_device());
+  int st = csr ? pad_decode_plan_csr(&d, static_cast<int>(num_splits), cus, &plan)
+               : pad_decode_plan(&d, static_cast<int>(num_splits), cus, &plan);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
-  void* ws_ptr = nullptr;
-  int32_t* counters = nullptr;
+  pad_decode_call c;
+  std::memset(&c, 0, sizeof(c));
+  c.q = q.data_ptr();
+  c.k_cache = k_cache.data_ptr();
+  c.v_cache = v_cache.data_ptr();
+  c.block_table = ix.ids;
+  c.seq_lens = ix.seq_lens;
+  c.indptr = ix.indptr;
+  c.last_page_len = ix.last_page_len;
+  c.out = out.data_ptr();
   if (!plan.single_pass) {
     StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
-    ws_ptr = sc.workspace.data_ptr();
-    counters = sc.counters.data_ptr<int32_t>();
+    c.workspace = sc.workspace.data_ptr();
+    c.workspace_bytes = plan.workspace_bytes;
+    c.counters = sc.counters.data_ptr<int32_t>();
+    c.num_counters = plan.counters;
   }
-  st = pad_decode_launch_csr(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), indices.data_ptr<int32_t>(),
-                             indptr.data_ptr<int32_t>(), last_page_len.data_ptr<int32_t>(), out.data_ptr(), ws_ptr,
-                             plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
-                             static_cast<int>(num_splits), static_cast<int>(engine), stream);
+  if (worklist.defined()) {
+    c.worklist = worklist.data_ptr();
+    c.worklist_bytes = static_cast<size_t>(worklist.numel());
+  }
+  c.scale = static_cast<float>(scale);
+  c.num_splits = static_cast<int32_t>(num_splits);
+  c.engine = static_cast<int32_t>(engine);
+  c.kv_format = kv_format;
+  c.k_scale = static_cast<float>(k_scale);
+  c.v_scale = static_cast<float>(v_scale);
+  st = pad_decode_launch_call(&c, &d, stream);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   return out;
 }
 
-// Plan once, run many (pad_decode_plan_worklist / pad_decode_launch_worklist):
+// Decode with a CSR page index: the page ids of sequence b are
+// indices[indptr[b] : indptr[b+1]] and its last page holds last_page_len[b]
+// tokens (the (indptr, indices, last_page_len) triple the reference's
+// FlashInfer adapter builds, src/flashinfer_adapter.py:40-65).  fp16 or fp8
+// caches (k_scale / v_scale are read for fp8 only).
+torch::Tensor forward_csr(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache, torch::Tensor indptr,
+                          torch::Tensor indices, torch::Tensor last_page_len, double scale, int64_t num_splits,
+                          int64_t engine, double k_scale, double v_scale) {
+  const int fmt = cache_format(q, k_cache, v_cache);
+  check_csr(q, k_cache, v_cache, indptr, indices, last_page_len);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+  pad_decode_dims d;
+  csr_dims(q, k_cache, v_cache, indices, last_page_len, out, &d);
+  return launch_call(q, k_cache, v_cache, out, d, csr_index(indptr, indices, last_page_len), torch::Tensor(), scale,
+                     num_splits, engine, fmt, k_scale, v_scale);
+}
+
+// Plan once, run many (pad_decode_plan_worklist_call / pad_decode_launch_call):
 // the dims of a decode with these index tensors and head/page geometry.
 // q/k/v/out strides do not enter the plan; num_pages only bounds page ids at
 // run time, so the plan uses any positive value.
@@ -296,18 +380,37 @@ pad_decode_dims worklist_dims(int64_t batch, int64_t num_q_heads, int64_t num_kv
   return d;
 }
 
-torch::Tensor new_worklist(const torch::Tensor& like, const pad_decode_dims& d, int64_t num_splits, bool csr) {
+// Writes the work list of the launch described by d, ix, num_splits and
+// kv_format into a new uint8 tensor on `like`'s device (current stream).
+torch::Tensor plan_call(const torch::Tensor& like, const pad_decode_dims& d, const PageIndex& ix,
+                        int64_t num_splits, int64_t kv_format) {
   c10::hip::HIPGuardMasqueradingAsCUDA guard(like.device());
+  const bool csr = ix.indptr != nullptr;
   size_t bytes = 0;
-  const int st = pad_decode_worklist_bytes(&d, static_cast<int>(num_splits), cached_cus(like.get_device()),
-                                           csr ? 1 : 0, &bytes);
+  int st = pad_decode_worklist_bytes(&d, static_cast<int>(num_splits), cached_cus(like.get_device()),
+                                     csr ? 1 : 0, &bytes);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  return torch::empty({static_cast<int64_t>(bytes)}, like.options().dtype(at::kByte));
+  torch::Tensor wl = torch::empty({static_cast<int64_t>(bytes)}, like.options().dtype(at::kByte));
+  pad_decode_call c;
+  std::memset(&c, 0, sizeof(c));
+  c.block_table = ix.ids;
+  c.seq_lens = ix.seq_lens;
+  c.indptr = ix.indptr;
+  c.last_page_len = ix.last_page_len;
+  c.num_splits = static_cast<int32_t>(num_splits);
+  c.kv_format = static_cast<int32_t>(kv_format);
+  c.k_scale = c.v_scale = 1.0f;
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(like.get_device()).stream();
+  st = pad_decode_plan_worklist_call(&c, &d, wl.data_ptr(), bytes, stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return wl;
 }
 
-// Work list of a dense-table decode (block_table [B, max_pages], seq_lens [B], int32 on the GPU).
+// Work list of a dense-table decode (block_table [B, max_pages], seq_lens
+// [B], int32 on the GPU) over caches of kv_format (PAD_KV_*).
 torch::Tensor plan_worklist(torch::Tensor block_table, torch::Tensor seq_lens, int64_t num_q_heads,
-                            int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_splits) {
+                            int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_splits,
+                            int64_t kv_format) {
   TORCH_CHECK(block_table.is_cuda() && seq_lens.is_cuda() && block_table.device() == seq_lens.device(),
               "pa_decode: block_table and seq_lens must be on the same GPU");
   TORCH_CHECK(block_table.scalar_type() == at::kInt && seq_lens.scalar_type() == at::kInt,
@@ -319,20 +422,14 @@ torch::Tensor plan_worklist(torch::Tensor block_table, torch::Tensor seq_lens, i
   d.bt_stride[0] = block_table.stride(0);
   d.bt_stride[1] = block_table.stride(1);
   d.sl_stride = seq_lens.stride(0);
-  torch::Tensor wl = new_worklist(block_table, d, num_splits, false);
-  c10::hip::HIPGuardMasqueradingAsCUDA guard(block_table.device());
-  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(block_table.get_device()).stream();
-  const int st = pad_decode_plan_worklist(block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), &d,
-                                          static_cast<int>(num_splits), wl.data_ptr(),
-                                          static_cast<size_t>(wl.numel()), stream);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  return wl;
+  return plan_call(block_table, d, dense_index(block_table, seq_lens), num_splits, kv_format);
 }
 
-// Work list of a CSR decode (indptr [B + 1], indices [nnz], last_page_len [B], int32 on the GPU).
+// Work list of a CSR decode (indptr [B + 1], indices [nnz], last_page_len
+// [B], int32 on the GPU) over caches of kv_format.
 torch::Tensor plan_worklist_csr(torch::Tensor indptr, torch::Tensor indices, torch::Tensor last_page_len,
                                 int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
-                                int64_t num_splits) {
+                                int64_t num_splits, int64_t kv_format) {
   TORCH_CHECK(indptr.is_cuda() && indices.is_cuda() && last_page_len.is_cuda() &&
                   indptr.device() == indices.device() && indptr.device() == last_page_len.device(),
               "pa_decode: indptr, indices and last_page_len must be on the same GPU");
@@ -347,119 +444,41 @@ torch::Tensor plan_worklist_csr(torch::Tensor indptr, torch::Tensor indices, tor
   pad_decode_dims d = worklist_dims(last_page_len.size(0), num_q_heads, num_kv_heads, head_dim, page_size,
                                     indices.size(0));
   d.bt_stride[1] = 1;
-  torch::Tensor wl = new_worklist(indices, d, num_splits, true);
-  c10::hip::HIPGuardMasqueradingAsCUDA guard(indices.device());
-  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(indices.get_device()).stream();
-  const int st = pad_decode_plan_worklist_csr(indices.data_ptr<int32_t>(), indptr.data_ptr<int32_t>(),
-                                              last_page_len.data_ptr<int32_t>(), &d, static_cast<int>(num_splits),
-                                              wl.data_ptr(), static_cast<size_t>(wl.numel()), stream);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  return wl;
+  return plan_call(indices, d, csr_index(indptr, indices, last_page_len), num_splits, kv_format);
 }
 
-// Decode from a work list (dense table): same arguments and result as
-// forward() with engine 0, plus the list plan_worklist() wrote for them.
+// Decode from a work list (dense table): forward() with engine 0 (or
+// forward_kv8() for fp8 caches), plus the list plan_worklist() wrote for the
+// same index tensors and cache format.
 torch::Tensor forward_worklist(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
                                torch::Tensor block_table, torch::Tensor seq_lens, torch::Tensor worklist,
-                               double scale, int64_t num_splits) {
-  TORCH_CHECK(worklist.is_cuda() && worklist.device() == q.device() && worklist.scalar_type() == at::kByte &&
-                  worklist.is_contiguous(),
-              "pa_decode: worklist must be a contiguous uint8 tensor on q's device");
-  TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && block_table.is_cuda() &&
-                  seq_lens.is_cuda(),
-              "pa_decode: all tensors must be on the GPU");
-  TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() &&
-                  q.device() == block_table.device() && q.device() == seq_lens.device(),
-              "pa_decode: all tensors must be on the same device");
-  TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
-                  v_cache.scalar_type() == at::kHalf,
-              "pa_decode: q, k_cache and v_cache must be float16");
-  TORCH_CHECK(block_table.scalar_type() == at::kInt && seq_lens.scalar_type() == at::kInt,
-              "pa_decode: block_table and seq_lens must be int32");
-  TORCH_CHECK(q.dim() == 3 && k_cache.dim() == 4 && v_cache.sizes() == k_cache.sizes(),
-              "pa_decode: q must be [batch, num_q_heads, head_dim] and the caches 4-D and alike");
-  TORCH_CHECK(block_table.dim() == 2 && block_table.size(0) == q.size(0) && seq_lens.dim() == 1 &&
-                  seq_lens.size(0) == q.size(0),
-              "pa_decode: block_table must be [batch, max_pages] and seq_lens [batch]");
-  TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
+                               double scale, int64_t num_splits, double k_scale, double v_scale) {
+  check_worklist(q, worklist);
+  const int fmt = cache_format(q, k_cache, v_cache);
+  check_dense(q, k_cache, v_cache, block_table, seq_lens, k_cache.scalar_type());
   c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
   auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
   pad_decode_dims d;
   fill_dims(q, k_cache, v_cache, block_table, seq_lens, out, &d);
-  pad_decode_plan_t plan;
-  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cached_cus(q.get_device()), &plan);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
-  void* ws_ptr = nullptr;
-  int32_t* counters = nullptr;
-  if (!plan.single_pass) {
-    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
-    ws_ptr = sc.workspace.data_ptr();
-    counters = sc.counters.data_ptr<int32_t>();
-  }
-  st = pad_decode_launch_worklist(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                                  block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
-                                  ws_ptr, plan.workspace_bytes, counters, plan.counters, &d,
-                                  static_cast<float>(scale), static_cast<int>(num_splits), worklist.data_ptr(),
-                                  static_cast<size_t>(worklist.numel()), stream);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  return out;
+  return launch_call(q, k_cache, v_cache, out, d, dense_index(block_table, seq_lens), worklist, scale, num_splits,
+                     0, fmt, k_scale, v_scale);
 }
 
 // Decode from a work list (CSR index): forward_csr() with engine 0 plus the
-// list plan_worklist_csr() wrote for the same index tensors.
+// list plan_worklist_csr() wrote for the same index tensors and cache format.
 torch::Tensor forward_worklist_csr(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
                                    torch::Tensor indptr, torch::Tensor indices, torch::Tensor last_page_len,
-                                   torch::Tensor worklist, double scale, int64_t num_splits) {
-  TORCH_CHECK(worklist.is_cuda() && worklist.device() == q.device() && worklist.scalar_type() == at::kByte &&
-                  worklist.is_contiguous(),
-              "pa_decode: worklist must be a contiguous uint8 tensor on q's device");
-  TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && indptr.is_cuda() && indices.is_cuda() &&
-                  last_page_len.is_cuda(),
-              "pa_decode: all tensors must be on the GPU");
-  TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() && q.device() == indptr.device() &&
-                  q.device() == indices.device() && q.device() == last_page_len.device(),
-              "pa_decode: all tensors must be on the same device");
-  TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
-                  v_cache.scalar_type() == at::kHalf,
-              "pa_decode: q, k_cache and v_cache must be float16");
-  TORCH_CHECK(indptr.scalar_type() == at::kInt && indices.scalar_type() == at::kInt &&
-                  last_page_len.scalar_type() == at::kInt,
-              "pa_decode: indptr, indices and last_page_len must be int32");
-  TORCH_CHECK(q.dim() == 3 && k_cache.dim() == 4 && v_cache.sizes() == k_cache.sizes(),
-              "pa_decode: q must be [batch, num_q_heads, head_dim] and the caches 4-D and alike");
-  TORCH_CHECK(indptr.dim() == 1 && indptr.size(0) == q.size(0) + 1 && last_page_len.dim() == 1 &&
-                  last_page_len.size(0) == q.size(0) && indices.dim() == 1 && indices.is_contiguous() &&
-                  indptr.is_contiguous() && last_page_len.is_contiguous(),
-              "pa_decode: indptr [batch + 1], indices [nnz] and last_page_len [batch] must be contiguous");
-  TORCH_CHECK(indices.size(0) <= INT32_MAX, "pa_decode: too many page ids");
-  TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
+                                   torch::Tensor worklist, double scale, int64_t num_splits, double k_scale,
+                                   double v_scale) {
+  check_worklist(q, worklist);
+  const int fmt = cache_format(q, k_cache, v_cache);
+  check_csr(q, k_cache, v_cache, indptr, indices, last_page_len);
   c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
   auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
   pad_decode_dims d;
-  fill_dims(q, k_cache, v_cache, indices.view({1, -1}), last_page_len, out, &d);
-  d.max_pages = static_cast<int32_t>(indices.size(0));
-  d.bt_stride[0] = 0;
-  d.bt_stride[1] = 1;
-  pad_decode_plan_t plan;
-  int st = pad_decode_plan_csr(&d, static_cast<int>(num_splits), cached_cus(q.get_device()), &plan);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
-  void* ws_ptr = nullptr;
-  int32_t* counters = nullptr;
-  if (!plan.single_pass) {
-    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
-    ws_ptr = sc.workspace.data_ptr();
-    counters = sc.counters.data_ptr<int32_t>();
-  }
-  st = pad_decode_launch_worklist_csr(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                                      indices.data_ptr<int32_t>(), indptr.data_ptr<int32_t>(),
-                                      last_page_len.data_ptr<int32_t>(), out.data_ptr(), ws_ptr,
-                                      plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
-                                      static_cast<int>(num_splits), worklist.data_ptr(),
-                                      static_cast<size_t>(worklist.numel()), stream);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  return out;
+  csr_dims(q, k_cache, v_cache, indices, last_page_len, out, &d);
+  return launch_call(q, k_cache, v_cache, out, d, csr_index(indptr, indices, last_page_len), worklist, scale,
+                     num_splits, 0, fmt, k_scale, v_scale);
 }
 
 // Same argument list as the reference's forward_v4 binding
@@ -516,18 +535,33 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "v_scale, num_splits) -> out");
   m.def("forward_csr", &forward_csr,
         "Paged-attention decode over a CSR page index (q, k_cache, v_cache, indptr, indices, last_page_len, "
-        "scale, num_splits, engine) -> out");
+        "scale, num_splits, engine, k_scale=1, v_scale=1) -> out; fp16 or fp8 caches",
+        py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("indptr"), py::arg("indices"),
+        py::arg("last_page_len"), py::arg("scale"), py::arg("num_splits"), py::arg("engine"),
+        py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0);
   m.def("plan", &plan, "Split plan for the given shapes (host only)");
   m.def("plan_worklist", &plan_worklist,
         "Work list of a dense-table decode (block_table, seq_lens, num_q_heads, num_kv_heads, head_dim, "
-        "page_size, num_splits) -> uint8 tensor");
+        "page_size, num_splits, kv_format=0) -> uint8 tensor",
+        py::arg("block_table"), py::arg("seq_lens"), py::arg("num_q_heads"), py::arg("num_kv_heads"),
+        py::arg("head_dim"), py::arg("page_size"), py::arg("num_splits"), py::arg("kv_format") = 0);
   m.def("plan_worklist_csr", &plan_worklist_csr,
         "Work list of a CSR decode (indptr, indices, last_page_len, num_q_heads, num_kv_heads, head_dim, "
-        "page_size, num_splits) -> uint8 tensor");
+        "page_size, num_splits, kv_format=0) -> uint8 tensor",
+        py::arg("indptr"), py::arg("indices"), py::arg("last_page_len"), py::arg("num_q_heads"),
+        py::arg("num_kv_heads"), py::arg("head_dim"), py::arg("page_size"), py::arg("num_splits"),
+        py::arg("kv_format") = 0);
   m.def("forward_worklist", &forward_worklist,
-        "Decode from a work list (q, k_cache, v_cache, block_table, seq_lens, worklist, scale, num_splits) -> out");
+        "Decode from a work list (q, k_cache, v_cache, block_table, seq_lens, worklist, scale, num_splits, "
+        "k_scale=1, v_scale=1) -> out; fp16 or fp8 caches",
+        py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("block_table"), py::arg("seq_lens"),
+        py::arg("worklist"), py::arg("scale"), py::arg("num_splits"), py::arg("k_scale") = 1.0,
+        py::arg("v_scale") = 1.0);
   m.def("forward_worklist_csr", &forward_worklist_csr,
         "Decode from a work list (q, k_cache, v_cache, indptr, indices, last_page_len, worklist, scale, "
-        "num_splits) -> out");
+        "num_splits, k_scale=1, v_scale=1) -> out; fp16 or fp8 caches",
+        py::arg("q"), py::arg("k_cache"), py::arg("v_cache"), py::arg("indptr"), py::arg("indices"),
+        py::arg("last_page_len"), py::arg("worklist"), py::arg("scale"), py::arg("num_splits"),
+        py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0);
   m.def("abi_version", &pad_decode_abi_version, "C ABI version of the linked libpa_decode.so");
 }

@@ -51,7 +51,7 @@ def test_library_exports_every_declared_symbol():
     lib = _native.capi()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.pad_decode_abi_version() == 5
+    assert lib.pad_decode_abi_version() == 6
 
 
 def test_status_strings():
@@ -462,3 +462,65 @@ def test_fp8_plan_keeps_the_scratch_of_the_fp16_plan():
         assert b.waves_per_group >= a.waves_per_group
         if d != 128:
             assert b.waves_per_group == a.waves_per_group
+
+
+def test_call_descriptor_layout_matches_the_header(tmp_path):
+    # The ctypes mirror of pad_decode_call (and pad_decode_dims, pad_decode_plan_t)
+    # has the C compiler's field offsets and size for the header as written.
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    structs = {"pad_decode_call": _native.PadCall, "pad_decode_dims": _native.PadDims,
+               "pad_decode_plan_t": _native.PadPlan}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "pa_decode.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-std=c99", f"-I{os.path.dirname(HEADER)}", str(src), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    for line in filter(None, got):
+        cname, field, value = line.split()
+        py = structs[cname]
+        want = ctypes.sizeof(py) if field == "sizeof" else getattr(py, field).offset
+        assert int(value) == want, (cname, field, int(value), want)
+
+
+def test_launch_call_checks_on_the_host():
+    # The descriptor entry answers argument problems before any device call.
+    lib = _native.capi()
+    fake = 256
+    dm = _dims(batch=2, max_pages=4)
+    c = _native.PadCall(q=fake, k_cache=fake, v_cache=fake, block_table=fake, seq_lens=fake, out=fake, scale=0.1,
+                        num_splits=1, engine=0, kv_format=0, k_scale=1.0, v_scale=1.0)
+    assert lib.pad_decode_launch_call(None, ctypes.byref(dm), None) == 1
+    half_csr = _native.PadCall.from_buffer_copy(c)
+    half_csr.indptr = fake  # CSR needs indptr and last_page_len together
+    assert lib.pad_decode_launch_call(ctypes.byref(half_csr), ctypes.byref(dm), None) == 1
+    wl_valu = _native.PadCall.from_buffer_copy(c)
+    wl_valu.worklist, wl_valu.worklist_bytes, wl_valu.engine = fake, 1 << 20, 1
+    assert lib.pad_decode_launch_call(ctypes.byref(wl_valu), ctypes.byref(dm), None) == 2
+    for fmt, ks, engine, code in ((3, 1.0, 0, 12), (1, 0.0, 0, 12), (1, 1.0, 1, 12), (2, float("inf"), 0, 12)):
+        bad = _native.PadCall.from_buffer_copy(c)
+        bad.kv_format, bad.k_scale, bad.engine = fmt, ks, engine
+        assert lib.pad_decode_launch_call(ctypes.byref(bad), ctypes.byref(dm), None) == code, (fmt, ks, engine)
+    dm96 = _dims(batch=2, max_pages=4, d=96)
+    fp8 = _native.PadCall.from_buffer_copy(c)
+    fp8.kv_format = 1
+    assert lib.pad_decode_launch_call(ctypes.byref(fp8), ctypes.byref(dm96), None) == 3
+    # Planning a work list: NULL descriptor, VALU engine, bad format.
+    wl = ctypes.create_string_buffer(1 << 16)
+    assert lib.pad_decode_plan_worklist_call(None, ctypes.byref(dm), wl, len(wl), None) == 1
+    valu = _native.PadCall.from_buffer_copy(c)
+    valu.engine = 1
+    assert lib.pad_decode_plan_worklist_call(ctypes.byref(valu), ctypes.byref(dm), wl, len(wl), None) == 2
+    badf = _native.PadCall.from_buffer_copy(c)
+    badf.kv_format = 7
+    assert lib.pad_decode_plan_worklist_call(ctypes.byref(badf), ctypes.byref(dm), wl, len(wl), None) == 12

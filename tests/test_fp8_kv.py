@@ -27,7 +27,7 @@ import pytest
 import torch
 
 from oracle.reference import decode_fp8_protocol
-from paged_attention_decode_amd import _native
+from paged_attention_decode_amd import _native, heuristics
 from tests.helpers import assert_parity, make_cache, shuffled_table
 
 pytestmark = pytest.mark.gpu
@@ -265,3 +265,146 @@ def test_fp8_graph_capture_replays():
             torch.cuda.synchronize()
             assert torch.equal(out_static, eager), f"replay {rep} differs from the eager call"
     assert_parity(out_static.cpu(), decode_fp8_protocol(qs[-1].float().cpu(), k8, v8, bt, sl, ks, vs))
+
+
+def _csr_of(bt, sl, ps):
+    from oracle.csr import paged_kv_indices as ref_indices
+
+    return [t.cuda() for t in ref_indices(bt, sl, ps)]
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("ps", [16, 4, 12])
+def test_fp8_csr_matches_oracle_and_fp16_csr(fmt, ps):
+    # The CSR entry over fp8 caches: oracle parity with scales, and at unit
+    # scales the fp16 CSR call on the widened codes, bit for bit.
+    import paged_attention_decode_amd as pad
+
+    lens = [1, ps + 3, 150, 777, 0, 2000]
+    q, k, v, bt, sl = _case(lens, ps, 2, 6, 128, seed=ps + 7)
+    indptr, indices, last = _csr_of(bt, sl, ps)
+    ks, vs = float(k.abs().max()) / 300.0, float(v.abs().max()) / 111.0
+    k8, v8 = _quant(k, fmt, ks), _quant(v, fmt, vs)
+    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs)
+    qd = q.half().cuda()
+    for splits in (None, 1, 5):
+        out = pad.paged_attention_decode_csr(qd, k8.cuda(), v8.cuda(), indptr, indices, last, num_splits=splits,
+                                             k_scale=ks, v_scale=vs)
+        torch.cuda.synchronize()
+        assert_parity(out.cpu(), expected)
+    k1, v1 = k.to(FMTS[fmt]), v.to(FMTS[fmt])
+    for splits in (None, 3):
+        a = pad.paged_attention_decode_csr(qd, k1.cuda(), v1.cuda(), indptr, indices, last, num_splits=splits)
+        b = pad.paged_attention_decode_csr(qd, k1.half().cuda(), v1.half().cuda(), indptr, indices, last,
+                                           num_splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), splits
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_fp8_wrapper_plan_once_run_many(fmt):
+    # BatchDecodeWrapper over fp8 caches: plan with kv_data_type, run with
+    # k_scale / v_scale; the same output as the one-shot fp8 calls (dense and
+    # CSR), for two steps of new q, and oracle parity.
+    import paged_attention_decode_amd as pad
+
+    lens = [4096, 300, 2500, 1, 777, 0, 1500, 64]
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=41)
+    ks, vs = float(k.abs().max()) / 300.0, float(v.abs().max()) / 111.0
+    k8, v8 = _quant(k, fmt, ks), _quant(v, fmt, vs)
+    kd, vd, btd, sld = k8.cuda(), v8.cuda(), bt.cuda(), sl.cuda()
+    indptr, indices, last = _csr_of(bt, sl, 16)
+    dense = pad.BatchDecodeWrapper()
+    dense.plan_block_table(btd, sld, 12, 2, 128, 16, kv_data_type=FMTS[fmt])
+    csr = pad.BatchDecodeWrapper()
+    csr.plan(indptr, indices, last, 12, 2, 128, 16, kv_data_type=fmt)
+    for step in range(2):
+        qd = (q if step == 0 else torch.randn(q.shape, generator=torch.Generator().manual_seed(42))).half().cuda()
+        a = dense.run(qd, (kd, vd), k_scale=ks, v_scale=vs)
+        b = pad.paged_attention_decode_fp8(qd, kd, vd, btd, sld, k_scale=ks, v_scale=vs)
+        c = csr.run(qd, (kd, vd), k_scale=ks, v_scale=vs)
+        d = pad.paged_attention_decode_csr(qd, kd, vd, indptr, indices, last, k_scale=ks, v_scale=vs)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b) and torch.equal(c, d), step
+        assert_parity(a.cpu(), decode_fp8_protocol(qd.float().cpu(), k8, v8, bt, sl, ks, vs))
+    # A wrapper planned for fp16 caches refuses fp8 ones.
+    w16 = pad.BatchDecodeWrapper()
+    w16.plan_block_table(btd, sld, 12, 2, 128, 16)
+    with pytest.raises(AssertionError, match="kv_data_type"):
+        w16.run(q.half().cuda(), (kd, vd), k_scale=ks, v_scale=vs)
+
+
+def test_fp8_launch_with_an_fp16_work_list_plans_in_the_kernel():
+    # A work list made for fp16 caches carries another plan key (the fp8
+    # launch runs 8-wave workgroups here), so the fp8 launch ignores it and
+    # plans in the kernel: the result is the one-shot fp8 call's.
+    import paged_attention_decode_amd as pad
+    from paged_attention_decode_amd._native import ext
+
+    lens = [4096] * 16  # bandwidth-bound: fp16 plans 4-wave, fp8 8-wave workgroups
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=43, spare=0, extra=0)
+    assert heuristics.plan(16, 12, 2, 128, 16, 256).waves_per_group == 4
+    assert heuristics.plan(16, 12, 2, 128, 16, 256, kv_bytes=1).waves_per_group == 8
+    k8, v8 = k.to(torch.float8_e4m3fn).cuda(), v.to(torch.float8_e4m3fn).cuda()
+    qd, btd, sld = q.half().cuda(), bt.cuda(), sl.cuda()
+    wl16 = ext().plan_worklist(btd, sld, 12, 2, 128, 16, 0, 0)
+    wl8 = ext().plan_worklist(btd, sld, 12, 2, 128, 16, 0, 1)
+    assert not torch.equal(wl16[:32], wl8[:32])  # different plan keys in the headers
+    scale = 1.0 / math.sqrt(128)
+    a = ext().forward_worklist(qd, k8, v8, btd, sld, wl16, scale, 0, 1.0, 1.0)
+    b = ext().forward_worklist(qd, k8, v8, btd, sld, wl8, scale, 0, 1.0, 1.0)
+    c = pad.paged_attention_decode_fp8(qd, k8, v8, btd, sld)
+    torch.cuda.synchronize()
+    assert torch.equal(a, c) and torch.equal(b, c)
+
+
+def test_launch_call_descriptor_through_the_c_abi():
+    # pad_decode_launch_call() runs what the dedicated entry points run: the
+    # fp16 dense call equals pad_decode_launch bit for bit, and an fp8 CSR
+    # call with a planned work list equals the binding's one-shot CSR call.
+    import paged_attention_decode_amd as pad
+
+    lib = _native.capi()
+    lens = [1, 77, 400, 1000, 2500]
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=44)
+    qd, kd, vd, btd, sld = q.half().cuda(), k.half().cuda(), v.half().cuda(), bt.cuda(), sl.cuda()
+    scale = 1.0 / math.sqrt(128)
+    stream = torch.cuda.current_stream().cuda_stream
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    counters = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    ref = torch.empty_like(qd)
+    dm = _native.dims_for(qd, kd, vd, btd, sld, ref)
+    assert lib.pad_decode_launch(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), btd.data_ptr(), sld.data_ptr(),
+                                 ref.data_ptr(), ws.data_ptr(), ws.numel(), counters.data_ptr(), counters.numel(),
+                                 ctypes.byref(dm), scale, 0, stream) == 0
+    out = torch.empty_like(qd)
+    c = _native.PadCall(q=qd.data_ptr(), k_cache=kd.data_ptr(), v_cache=vd.data_ptr(), block_table=btd.data_ptr(),
+                        seq_lens=sld.data_ptr(), out=out.data_ptr(), workspace=ws.data_ptr(),
+                        workspace_bytes=ws.numel(), counters=counters.data_ptr(), num_counters=counters.numel(),
+                        scale=scale, num_splits=0, engine=0, kv_format=0, k_scale=1.0, v_scale=1.0)
+    assert lib.pad_decode_launch_call(ctypes.byref(c), ctypes.byref(dm), stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    # fp8 codes with a CSR index and a work list planned through the descriptor.
+    ks, vs = float(k.abs().max()) / 300.0, float(v.abs().max()) / 111.0
+    k8, v8 = _quant(k, "e5m2", ks).cuda(), _quant(v, "e5m2", vs).cuda()
+    indptr, indices, last = _csr_of(bt, sl, 16)
+    out8 = torch.empty_like(qd)
+    d8 = _native.dims_for(qd, k8, v8, indices.view(1, -1), last, out8)
+    d8.max_pages, d8.bt_stride[0], d8.bt_stride[1] = indices.numel(), 0, 1
+    wlb = ctypes.c_size_t()
+    assert lib.pad_decode_worklist_bytes(ctypes.byref(d8), 0, 0, 1, ctypes.byref(wlb)) == 0
+    wl = torch.empty(wlb.value, dtype=torch.uint8, device="cuda")
+    c8 = _native.PadCall(q=qd.data_ptr(), k_cache=k8.data_ptr(), v_cache=v8.data_ptr(), block_table=indices.data_ptr(),
+                         indptr=indptr.data_ptr(), last_page_len=last.data_ptr(), out=out8.data_ptr(),
+                         workspace=ws.data_ptr(), workspace_bytes=ws.numel(), counters=counters.data_ptr(),
+                         num_counters=counters.numel(), worklist=wl.data_ptr(), worklist_bytes=wl.numel(),
+                         scale=scale, num_splits=0, engine=0, kv_format=2, k_scale=ks, v_scale=vs)
+    assert lib.pad_decode_plan_worklist_call(ctypes.byref(c8), ctypes.byref(d8), wl.data_ptr(), wl.numel(),
+                                             stream) == 0
+    assert lib.pad_decode_launch_call(ctypes.byref(c8), ctypes.byref(d8), stream) == 0
+    want = pad.paged_attention_decode_csr(qd, k8, v8, indptr, indices, last, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert torch.equal(out8, want)
+    assert_parity(out8.cpu(), decode_fp8_protocol(q, k8.cpu(), v8.cpu(), bt, sl, ks, vs))
+    assert torch.all(counters == 0)
