@@ -19,6 +19,8 @@
  *   seq_lens    int32 [batch]
  *   out         fp16 [batch, num_q_heads, head_dim]
  * head_dim must be contiguous (stride 1) for q, k_cache, v_cache and out.
+ * pad_decode_launch_kv8() and pad_decode_launch_call() also take fp8
+ * (e4m3fn / e5m2) caches of the same layout, one byte per element.
  *
  * The library replaces the reference's native launcher
  *   torch::Tensor paged_attn_decode_cuda_v4_launch(q, k_cache, v_cache,
