@@ -62,7 +62,8 @@ What one run measures (one GPU; ``--gpus`` above 1 exits with a message):
   (float8_e4m3fn and float8_e5m2 codes of the same C2 inputs, per-tensor
   scales; ``paged_attention_decode_fp8``), cold throughput in GB/s of its
   own algorithmic bytes (one byte per K/V element), the time ratio to the
-  fp16 headline, and batch 1 by the reference's latency method.  Not the
+  fp16 headline, and batch 1 by the reference's latency method; and
+  ``c2_bf16``, the same step in bfloat16 (q, caches and output).  Not the
   metric, which is quoted on fp16 caches.
 * ``cpu_baseline_configs`` (``--cpu-configs``, by default C1, C3, C4 and
   C5; ``none`` skips it): the CPU oracle next to the GPU call on each listed
@@ -584,6 +585,19 @@ def main():
                 "b1_us_per_call_warm": round(lat1, 2),
             }
             del rs, first, w1
+        # bfloat16 q, caches and output: the same bytes as the fp16 step.
+        first = wl.to_bf16(wl.make("C2", batch=args.batch, seed=1000))
+        rs = [first] + [wl.to_bf16(wl.make("C2", batch=args.batch, seed=1000 + i))
+                        for i in range(1, _rotation(first.k_cache.numel() * 4))]
+        tb = _throughput(pad, rs, engine, splits, args.steps, args.warmup)
+        result["c2_bf16"] = {
+            "workload": f"C2 batch {args.batch} in bfloat16 (q, caches, output); cold rotation",
+            "us_per_call_cold": round(tb * 1e6, 2),
+            "gbs_cold": round(wl.bytes_of(first) / tb / 1e9, 1),
+            "pct_of_peak_cold": round(100 * wl.bytes_of(first) / tb / 1e9 / PEAK_GBS, 2),
+            "time_vs_fp16_headline": round(tb / sec, 3),
+        }
+        del rs, first
         result["c2_fp8"] = {
             "workload": f"C2 batch {args.batch} with fp8 K/V caches (per-tensor scales, codes spanning 7/8 of the "
                         "range); cold rotation; q and output fp16",

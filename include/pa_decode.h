@@ -20,7 +20,8 @@
  *   out         fp16 [batch, num_q_heads, head_dim]
  * head_dim must be contiguous (stride 1) for q, k_cache, v_cache and out.
  * pad_decode_launch_kv8() and pad_decode_launch_call() also take fp8
- * (e4m3fn / e5m2) caches of the same layout, one byte per element.
+ * (e4m3fn / e5m2) caches of the same layout, one byte per element, and
+ * pad_decode_launch_call() bfloat16 q, caches and out (PAD_KV_BF16).
  *
  * The library replaces the reference's native launcher
  *   torch::Tensor paged_attn_decode_cuda_v4_launch(q, k_cache, v_cache,
@@ -83,15 +84,20 @@ typedef enum pad_status {
   PAD_ERR_DEVICE = 10,           /* no usable device / device query failed */
   PAD_ERR_SCRATCH_LIMIT = 11,    /* pad_decode_launch_noalloc: the call needs
                                     more than its static scratch holds      */
-  PAD_ERR_KV_FORMAT = 12         /* pad_decode_launch_kv8: unknown cache
-                                    format, or a scale that is not finite
-                                    and positive                            */
+  PAD_ERR_KV_FORMAT = 12         /* unknown cache format, a format the
+                                    entry point or engine does not take, or
+                                    an fp8 scale that is not finite and
+                                    positive                                */
 } pad_status;
 
-/* Element formats of the K/V caches (pad_decode_launch_kv8). */
+/* Element formats of the K/V caches (pad_decode_launch_kv8,
+ * pad_decode_launch_call).  fp8 caches pair with fp16 q and out. */
 #define PAD_KV_FP16 0         /* IEEE half (every other entry point)          */
 #define PAD_KV_FP8_E4M3FN 1   /* OCP fp8 E4M3 "fn": bias 7, no infinities     */
 #define PAD_KV_FP8_E5M2 2     /* OCP fp8 E5M2: bias 15, IEEE-like             */
+#define PAD_KV_BF16 3         /* bfloat16 q, caches and out (pad_decode_launch_call;
+                                 MFMA engine, every head_dim; P is rounded to
+                                 bf16 for the PV product)                     */
 
 /* Static scratch of pad_decode_launch_noalloc(), per device: fp32 partials
  * and int32 arrival counters.  48 MiB in all, held until the process ends. */
@@ -336,10 +342,12 @@ int pad_decode_launch_worklist_csr(const void* q, const void* k_cache,
  *     pad_decode_launch_csr();
  *   worklist / worklist_bytes: optional, a list planned for the same call
  *     (pad_decode_plan_worklist_call()); NULL plans in the kernel;
- *   engine: 0 (MFMA) or 1 (VALU: fp16 caches, no work list;
- *     PAD_ERR_INVALID_SHAPE otherwise, PAD_ERR_KV_FORMAT with fp8);
- *   kv_format, k_scale, v_scale: as pad_decode_launch_kv8(); the scales are
- *     ignored for PAD_KV_FP16.
+ *   engine: 0 (MFMA) or 1 (VALU: fp16 only, no work list;
+ *     PAD_ERR_INVALID_SHAPE with a work list, PAD_ERR_KV_FORMAT with fp8
+ *     or bf16);
+ *   kv_format, k_scale, v_scale: PAD_KV_FP16, PAD_KV_BF16 (q, caches and
+ *     out all bfloat16), or an fp8 cache format as pad_decode_launch_kv8();
+ *     the scales are read for fp8 only.
  * pad_decode_launch_call() runs exactly what the matching entry point runs:
  * pad_decode_launch_ex (no events), _csr, _worklist, _worklist_csr or _kv8,
  * with the same workspace and counters.  No counterpart in the reference. */

@@ -113,6 +113,19 @@ def decode_fp16_protocol(q, k_cache, v_cache, block_table, seq_lens, scale=None)
                                             seq_lens.detach().to("cpu"), scale)
 
 
+def decode_bf16_protocol(q, k_cache, v_cache, block_table, seq_lens, scale=None):
+    """Oracle on bfloat16-rounded inputs upcast to fp32 (the fp16 protocol with bf16 rounding).
+
+    The reference computes in fp16 only (src/kernel_cuda_v4.py:37-48); this
+    applies its oracle to the values a bfloat16 caller holds.
+    """
+    q32 = q.detach().to("cpu").bfloat16().float()
+    k32 = k_cache.detach().to("cpu").bfloat16().float()
+    v32 = v_cache.detach().to("cpu").bfloat16().float()
+    return paged_attention_decode_reference(q32, k32, v32, block_table.detach().to("cpu"),
+                                            seq_lens.detach().to("cpu"), scale)
+
+
 def decode_fp8_protocol(q, k_cache, v_cache, block_table, seq_lens, k_scale=1.0, v_scale=1.0, scale=None):
     """Oracle for fp8 caches: the fp32 oracle on the dequantised caches.
 

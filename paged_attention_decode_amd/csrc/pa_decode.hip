@@ -408,16 +408,43 @@ constexpr int kModeGeneric = 0;
 constexpr int kModeUniform = 1;
 constexpr int kModeSubpage = 2;
 
-// Element formats of the K/V caches (template parameter KVF of the MFMA
-// engine): fp16, or an OCP fp8 format, widened to fp16 in registers where
-// compute() uses a block, so that everything downstream (K staging, both
-// MFMAs, the softmax) is the fp16 path.
+// Element formats (template parameter KVF of the MFMA engine): fp16; an
+// OCP fp8 cache format, widened to fp16 in registers where compute() uses a
+// block, so that everything downstream (K staging, both MFMAs, the softmax)
+// is the fp16 path; or bfloat16 q, caches and output, which run the same
+// path on bf16 MFMAs (P rounded to bf16, as fp16 P is to fp16).
 constexpr int kKvF16 = 0;
-constexpr int kKvE4M3 = 1;  // float8_e4m3fn
-constexpr int kKvE5M2 = 2;  // float8_e5m2
+constexpr int kKvE4M3 = 1;  // float8_e4m3fn caches, fp16 q and output
+constexpr int kKvE5M2 = 2;  // float8_e5m2 caches, fp16 q and output
+constexpr int kKvBF16 = 3;  // bfloat16 q, caches and output
 
 template <int KVF>
-constexpr int kv_elem_bytes() { return KVF == kKvF16 ? 2 : 1; }
+constexpr bool kv_is_fp8() { return KVF == kKvE4M3 || KVF == kKvE5M2; }
+template <int KVF>
+constexpr int kv_elem_bytes() { return kv_is_fp8<KVF>() ? 1 : 2; }
+
+// One 16x16x16 MFMA step on 16-bit operands held as fp16 vectors: fp16, or
+// the bit patterns of bfloat16 values (KVF == kKvBF16).
+template <int KVF>
+__device__ __forceinline__ f4_t mfma16(h4_t a, h4_t b, f4_t c) {
+  if constexpr (KVF == kKvBF16) {
+    typedef short s4_t __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4_t, a), __builtin_bit_cast(s4_t, b), c,
+                                                     0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+}
+
+// x rounded (to nearest even) to the output format, as 16 bits in an fp16
+// slot: fp16, or bfloat16 for KVF == kKvBF16.
+template <int KVF>
+__device__ __forceinline__ _Float16 round16(float x) {
+  if constexpr (KVF == kKvBF16)
+    return __builtin_bit_cast(_Float16, (__bf16)x);
+  else
+    return (_Float16)x;
+}
 
 // Four fp8 codes (one dword, element i in byte i) as four fp16 values (two
 // dwords: elements 0-1 in lo, 2-3 in hi) with gfx950's scaled conversions
@@ -457,7 +484,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   constexpr int DT = D / 16;  // PV output tiles; V halves per lane per token
   constexpr int NDW = DT / 2;
   constexpr int ES = kv_elem_bytes<KVF>();  // bytes per cache element
-  static_assert(KVF == kKvF16 || NDW % 2 == 0, "fp8 caches: head_dim a multiple of 64");
+  static_assert(!kv_is_fp8<KVF>() || NDW % 2 == 0, "fp8 caches: head_dim a multiple of 64");
   // A lane's DT halves of a token row are NSEG segments of SEG dwords, so
   // that the 16 lanes of a group read 16*SEG*4 contiguous bytes per load
   // instruction: half dt is head_dim slot dim(r16, dt) =
@@ -471,7 +498,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   constexpr int NDWR = NDW * ES / 2;
   using Tile = KVTile<D, ES>;
   auto load_slice = [](const char* p) -> HVec<NDWR> {
-    if constexpr (KVF != kKvF16) {
+    if constexpr (kv_is_fp8<KVF>()) {
       // fp8: the same segments at one byte per element, kept as codes.
       HVec<NDWR> r;
 #pragma unroll
@@ -496,7 +523,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
   };
   // A loaded row in the fp16 layout (fp8 codes: four per dword, widened).
   auto widen = [](const HVec<NDWR>& x) -> HVec<NDW> {
-    if constexpr (KVF == kKvF16) {
+    if constexpr (!kv_is_fp8<KVF>()) {
       return x;
     } else {
       HVec<NDW> r;
@@ -689,8 +716,8 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
         qk = qv[kp];
       const h4_t q_lo = __builtin_shufflevector(qk, qk, 0, 1, 2, 3);
       const h4_t q_hi = __builtin_shufflevector(qk, qk, 4, 5, 6, 7);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k_lo, q_lo, sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(k_hi, q_hi, sacc, 0, 0, 0);
+      sacc = mfma16<KVF>(k_lo, q_lo, sacc);
+      sacc = mfma16<KVF>(k_hi, q_hi, sacc);
     }
     float x[4];
 #pragma unroll
@@ -720,12 +747,28 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
       m_run = m_new;
     }
     h4_t ph;
-    float psum = 0.f;
+    float psum = 0.f;  // l accumulates the same rounded weights P.V uses
+    if constexpr (KVF == kKvBF16) {
+      // Pairs through the packed conversion; a rounded bf16 pair's floats
+      // are its high and low halves shifted into place.
+      typedef float f2_t __attribute__((ext_vector_type(2)));
+      typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+      uint32_t u[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const _Float16 p = (_Float16)exp2_fast(x[i] - m_run);
-      ph[i] = p;
-      psum += (float)p;  // l accumulates the same rounded weights P.V uses
+      for (int j = 0; j < 2; ++j) {
+        const f2_t pf = {exp2_fast(x[2 * j] - m_run), exp2_fast(x[2 * j + 1] - m_run)};
+        u[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pf, b2_t));
+        psum += __uint_as_float(u[j] << 16) + __uint_as_float(u[j] & 0xffff0000u);
+      }
+      typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+      ph = __builtin_bit_cast(h4_t, u2_t{u[0], u[1]});
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const _Float16 p = (_Float16)exp2_fast(x[i] - m_run);
+        ph[i] = p;
+        psum += (float)p;
+      }
     }
     l_run += psum;
     HVec<NDW> vr[4];
@@ -736,7 +779,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
       h4_t av;
 #pragma unroll
       for (int i = 0; i < 4; ++i) av[i] = vr[i].h(dt);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, ph, o[dt], 0, 0, 0);
+      o[dt] = mfma16<KVF>(av, ph, o[dt]);
     }
   };
 
@@ -1326,9 +1369,11 @@ __device__ __forceinline__ bool worklist_item(const Phase1Args& a, int g, int G,
 // Minimum waves per SIMD each phase-1 instantiation is compiled for (it
 // caps the registers per lane at 512 / waves).  The generic page-size mode
 // of head_dim 128 gets 2 (256 registers): its six prefetched page ids did
-// not fit 168 registers without one VGPR spilled to scratch.
-constexpr int phase1_waves_per_simd(int d, int engine, int mode) {
-  return engine == 0 ? (d <= 128 ? (d == 128 && mode == 0 ? 2 : 3) : 1) : 1;
+// not fit 168 registers without one VGPR spilled to scratch; so do the
+// bfloat16 sub-page modes of head_dim 128 (2 VGPRs spilled at page size 4).
+constexpr int phase1_waves_per_simd(int d, int engine, int mode, int kvf) {
+  const bool wide = d == 128 && (mode == 0 || (kvf == kKvBF16 && mode >= kModeSubpage));
+  return engine == 0 ? (d <= 128 ? (wide ? 2 : 3) : 1) : 1;
 }
 
 // Most waves in one workgroup.  head_dim 256 takes at most 4, so that each
@@ -1408,7 +1453,7 @@ __global__ __launch_bounds__(64) void pad_plan_kernel(const Phase1Args a, int32_
 // element format (fp16, or fp8 on the MFMA engine).
 template <int D, int MODE, int ENGINE, int GQA_T, int KVF = kKvF16>
 __global__ __launch_bounds__(max_group_waves(D) * 64)
-    __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE, MODE))))
+    __attribute__((amdgpu_waves_per_eu(phase1_waves_per_simd(D, ENGINE, MODE, KVF))))
 void pad_phase1_kernel(const Phase1Args a) {
 #ifdef PAD_TIMELINE
   const unsigned long long tl_entry = __builtin_amdgcn_s_memrealtime();
@@ -1540,10 +1585,10 @@ void pad_phase1_kernel(const Phase1Args a) {
     }
     if (nsplit == 1) {
       // Ls >= 1: the max token contributes 2^0.  fp8 caches: V's scale too.
-      const float inv = (KVF != kKvF16 ? a.v_fix : 1.f) / Ls;
+      const float inv = (kv_is_fp8<KVF>() ? a.v_fix : 1.f) / Ls;
       h4_t hv;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
+      for (int i = 0; i < 4; ++i) hv[i] = round16<KVF>(acc[i] * inv);
       *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + col) = hv;
     } else {
       const uint32_t r = (uint32_t)(my_split * gqa + row);
@@ -1628,10 +1673,10 @@ void pad_phase1_kernel(const Phase1Args a) {
     float m = kNegInf, l = 0.f;
     f4_t acc = (f4_t)0.f;
     merge_partials(o_rsrc, ml_rsrc, 0, count, stride, gqa, row, col, D, m, l, acc);
-    const float inv = (KVF != kKvF16 ? a.v_fix : 1.f) / l;
+    const float inv = (kv_is_fp8<KVF>() ? a.v_fix : 1.f) / l;
     h4_t hv;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) hv[i] = (_Float16)(acc[i] * inv);
+    for (int i = 0; i < 4; ++i) hv[i] = round16<KVF>(acc[i] * inv);
     *reinterpret_cast<h4_t*>(out_bh + (int64_t)row * a.soh + col) = hv;
   }
   if (threadIdx.x == 0) atomicExch(unit_counter, 0);
@@ -1850,10 +1895,10 @@ static hipError_t launch_p1(const Phase1Args& a, dim3 grid, int nw, size_t lds, 
   return hipGetLastError();
 }
 
-// fp8 caches (MFMA engine; head_dim 64, 128 or 256): block mode from the
-// page size, as for fp16.
+// fp8 caches (head_dim 64, 128 or 256) and bfloat16 (every head_dim), MFMA
+// engine: block mode from the page size, as for fp16.
 template <int D, int KVF>
-static hipError_t dispatch_fp8(const Phase1Args& a, dim3 grid, int nw, size_t lds, hipStream_t st) {
+static hipError_t dispatch_kvf(const Phase1Args& a, dim3 grid, int nw, size_t lds, hipStream_t st) {
   if (a.ps % kBlockTokens == 0) return launch_p1<D, kModeUniform, 0, 0, KVF>(a, grid, nw, lds, st);
   switch (a.ps) {
     case 1: return launch_p1<D, kModeSubpage + 0, 0, 0, KVF>(a, grid, nw, lds, st);
@@ -1866,11 +1911,15 @@ static hipError_t dispatch_fp8(const Phase1Args& a, dim3 grid, int nw, size_t ld
 }
 
 template <int KVF>
-static hipError_t dispatch_fp8_dim(const Phase1Args& a, int head_dim, dim3 grid, int nw, size_t lds, hipStream_t st) {
+static hipError_t dispatch_kvf_dim(const Phase1Args& a, int head_dim, dim3 grid, int nw, size_t lds, hipStream_t st) {
+  if constexpr (KVF == kKvBF16) {
+    if (head_dim == 32) return dispatch_kvf<32, KVF>(a, grid, nw, lds, st);
+    if (head_dim == 96) return dispatch_kvf<96, KVF>(a, grid, nw, lds, st);
+  }
   switch (head_dim) {
-    case 64: return dispatch_fp8<64, KVF>(a, grid, nw, lds, st);
-    case 128: return dispatch_fp8<128, KVF>(a, grid, nw, lds, st);
-    case 256: return dispatch_fp8<256, KVF>(a, grid, nw, lds, st);
+    case 64: return dispatch_kvf<64, KVF>(a, grid, nw, lds, st);
+    case 128: return dispatch_kvf<128, KVF>(a, grid, nw, lds, st);
+    case 256: return dispatch_kvf<256, KVF>(a, grid, nw, lds, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -2043,10 +2092,11 @@ static size_t worklist_bytes_for(const pad_decode_plan_t& plan, const pad_decode
   return sizeof(int32_t) * (size_t)(kWlHeaderInts + kWlRecordInts * G);
 }
 
-// fp8 caches: a known format, the MFMA engine, head_dim 64/128/256 and
-// finite positive scales (the scales are not read for fp16).
+// A known format; bfloat16 and fp8 on the MFMA engine; fp8 with head_dim
+// 64/128/256 and finite positive scales (the scales are read for fp8 only).
 static int check_kv_format(int kv_format, int engine, const pad_decode_dims* d, float k_scale, float v_scale) {
   if (kv_format == PAD_KV_FP16) return PAD_OK;
+  if (kv_format == PAD_KV_BF16) return engine == 0 ? PAD_OK : PAD_ERR_KV_FORMAT;
   if (kv_format != PAD_KV_FP8_E4M3FN && kv_format != PAD_KV_FP8_E5M2) return PAD_ERR_KV_FORMAT;
   if (engine != 0) return PAD_ERR_KV_FORMAT;
   if (d && d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return PAD_ERR_UNSUPPORTED_HEAD_DIM;
@@ -2065,10 +2115,11 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   int st = check_kv_format(kv_format, engine, d, k_scale, v_scale);
   if (st != PAD_OK) return st;
   Launch L;
+  const bool fp8 = kv_format == PAD_KV_FP8_E4M3FN || kv_format == PAD_KV_FP8_E5M2;
   st = setup_launch(q, k, v, bt, sl, indptr, lpl, out, ws, ws_bytes, counters, num_counters, d, scale,
-                    num_splits, engine, true, &L, kv_format == PAD_KV_FP16 ? 2 : 1);
+                    num_splits, engine, true, &L, fp8 ? 1 : 2);
   if (st != PAD_OK || L.empty) return st;
-  if (kv_format != PAD_KV_FP16) {
+  if (fp8) {
     // The caches hold K / k_scale and V / v_scale: k_scale multiplies every
     // score, v_scale every output row.
     L.a.scale_log2 *= k_scale;
@@ -2086,9 +2137,11 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
     return PAD_ERR_LAUNCH;
   hipError_t e;
   if (kv_format == PAD_KV_FP8_E4M3FN) {
-    e = dispatch_fp8_dim<kKvE4M3>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
+    e = dispatch_kvf_dim<kKvE4M3>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
   } else if (kv_format == PAD_KV_FP8_E5M2) {
-    e = dispatch_fp8_dim<kKvE5M2>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
+    e = dispatch_kvf_dim<kKvE5M2>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
+  } else if (kv_format == PAD_KV_BF16) {
+    e = dispatch_kvf_dim<kKvBF16>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
   } else switch (d->head_dim) {
     case 32: e = dispatch_phase1<32>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
     case 64: e = dispatch_phase1<64>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
@@ -2249,7 +2302,8 @@ int pad_decode_launch_kv8(const void* q, const void* k_cache, const void* v_cach
                           const int32_t* seq_lens, void* out, void* workspace, size_t workspace_bytes,
                           int32_t* counters, int64_t num_counters, const pad_decode_dims* dims, float scale,
                           int kv_format, float k_scale, float v_scale, int num_splits, void* stream) {
-  if (kv_format == PAD_KV_FP16) return PAD_ERR_KV_FORMAT;  // fp16 caches: pad_decode_launch
+  // fp16 caches: pad_decode_launch; bfloat16: pad_decode_launch_call
+  if (kv_format != PAD_KV_FP8_E4M3FN && kv_format != PAD_KV_FP8_E5M2) return PAD_ERR_KV_FORMAT;
   return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, nullptr, nullptr, out, workspace,
                           workspace_bytes, counters, num_counters, dims, scale, num_splits, 0, nullptr, stream,
                           nullptr, 0, kv_format, k_scale, v_scale);
@@ -2324,9 +2378,9 @@ int pad_decode_plan_worklist_call(const pad_decode_call* c, const pad_decode_dim
   if (c->engine != 0) return PAD_ERR_INVALID_SHAPE;  // work lists serve the MFMA engine
   const int st = pad::check_kv_format(c->kv_format, 0, dims, c->k_scale, c->v_scale);
   if (st != PAD_OK) return st;
+  const bool fp8 = c->kv_format == PAD_KV_FP8_E4M3FN || c->kv_format == PAD_KV_FP8_E5M2;
   return pad::plan_worklist_impl(c->block_table, csr ? nullptr : c->seq_lens, c->indptr, c->last_page_len, dims,
-                                 c->num_splits, worklist, worklist_bytes, stream,
-                                 c->kv_format == PAD_KV_FP16 ? 2 : 1);
+                                 c->num_splits, worklist, worklist_bytes, stream, fp8 ? 1 : 2);
 }
 
 int pad_decode_counters_init(int32_t* counters, int64_t num_counters, void* stream) {
@@ -2365,7 +2419,7 @@ const char* pad_status_string(int status) {
              "(PAD_NOALLOC_WORKSPACE_BYTES of partials, PAD_NOALLOC_COUNTERS counters); use pad_decode_launch";
     case PAD_ERR_KV_FORMAT:
       return "unsupported K/V cache format or scale (fp8: PAD_KV_FP8_E4M3FN or PAD_KV_FP8_E5M2, MFMA engine, "
-             "finite positive k_scale and v_scale)";
+             "finite positive k_scale and v_scale; PAD_KV_BF16: MFMA engine)";
     default: return "unknown status";
   }
 }

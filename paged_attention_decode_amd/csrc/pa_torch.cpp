@@ -122,24 +122,15 @@ void fill_dims(const torch::Tensor& q, const torch::Tensor& k, const torch::Tens
   for (int i = 0; i < 3; ++i) d->out_stride[i] = out.stride(i);
 }
 
-// Checks shared by the dense-table entries; the caches hold cache_dtype.
+// Checks shared by the dense-table entries (dtypes are cache_format()'s).
 void check_dense(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache,
-                 const torch::Tensor& block_table, const torch::Tensor& seq_lens, at::ScalarType cache_dtype) {
+                 const torch::Tensor& block_table, const torch::Tensor& seq_lens) {
   TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && block_table.is_cuda() &&
                   seq_lens.is_cuda(),
               "pa_decode: all tensors must be on the GPU");
   TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() &&
                   q.device() == block_table.device() && q.device() == seq_lens.device(),
               "pa_decode: all tensors must be on the same device");
-  if (cache_dtype == at::kHalf) {
-    TORCH_CHECK(q.scalar_type() == at::kHalf && k_cache.scalar_type() == at::kHalf &&
-                    v_cache.scalar_type() == at::kHalf,
-                "pa_decode: q, k_cache and v_cache must be float16");
-  } else {
-    TORCH_CHECK(q.scalar_type() == at::kHalf, "pa_decode: q must be float16");
-    TORCH_CHECK(k_cache.scalar_type() == cache_dtype && v_cache.scalar_type() == cache_dtype,
-                "pa_decode: k_cache and v_cache must both be float8_e4m3fn or both float8_e5m2");
-  }
   TORCH_CHECK(block_table.scalar_type() == at::kInt && seq_lens.scalar_type() == at::kInt,
               "pa_decode: block_table and seq_lens must be int32");
   TORCH_CHECK(q.dim() == 3, "pa_decode: q must be [batch, num_q_heads, head_dim]");
@@ -151,115 +142,22 @@ void check_dense(const torch::Tensor& q, const torch::Tensor& k_cache, const tor
   TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
 }
 
-torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
-                      torch::Tensor block_table, torch::Tensor seq_lens, double scale,
-                      int64_t num_splits, int64_t engine) {
-  check_dense(q, k_cache, v_cache, block_table, seq_lens, at::kHalf);
-  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
-  pad_decode_dims d;
-  fill_dims(q, k_cache, v_cache, block_table, seq_lens, out, &d);
-
-  const int cus = cached_cus(q.get_device());
-  pad_decode_plan_t plan;
-  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cus, &plan);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
-  void* ws_ptr = nullptr;
-  int32_t* counters = nullptr;
-  if (!plan.single_pass) {
-    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
-    ws_ptr = sc.workspace.data_ptr();
-    counters = sc.counters.data_ptr<int32_t>();
-  }
-  st = pad_decode_launch_ex(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                            block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
-                            ws_ptr, plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
-                            static_cast<int>(num_splits), static_cast<int>(engine), nullptr, stream);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  return out;
-}
-
-// Decode over fp8 caches (torch.float8_e4m3fn or torch.float8_e5m2, both
-// caches the same) holding K / k_scale and V / v_scale; q and the output
-// stay fp16.  Same plan, scratch and stream as forward().
-torch::Tensor forward_kv8(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
-                          torch::Tensor block_table, torch::Tensor seq_lens, double scale, double k_scale,
-                          double v_scale, int64_t num_splits) {
-  const at::ScalarType kt = k_cache.scalar_type();
-  TORCH_CHECK(kt == at::kFloat8_e4m3fn || kt == at::kFloat8_e5m2,
-              "pa_decode: forward_kv8 needs float8_e4m3fn or float8_e5m2 caches");
-  check_dense(q, k_cache, v_cache, block_table, seq_lens, kt);
-  const int fmt = kt == at::kFloat8_e4m3fn ? PAD_KV_FP8_E4M3FN : PAD_KV_FP8_E5M2;
-  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
-  pad_decode_dims d;
-  fill_dims(q, k_cache, v_cache, block_table, seq_lens, out, &d);
-
-  const int cus = cached_cus(q.get_device());
-  pad_decode_plan_t plan;
-  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cus, &plan);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
-  void* ws_ptr = nullptr;
-  int32_t* counters = nullptr;
-  if (!plan.single_pass) {
-    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
-    ws_ptr = sc.workspace.data_ptr();
-    counters = sc.counters.data_ptr<int32_t>();
-  }
-  st = pad_decode_launch_kv8(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                             block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
-                             ws_ptr, plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
-                             fmt, static_cast<float>(k_scale), static_cast<float>(v_scale),
-                             static_cast<int>(num_splits), stream);
-  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
-  return out;
-}
-
-// PAD_KV_* format of the caches: both float16, or both the same fp8 type
-// (float8_e4m3fn / float8_e5m2); q is float16.
+// PAD_KV_* format of a call: float16 q with float16 or fp8 (float8_e4m3fn /
+// float8_e5m2) caches, or bfloat16 q with bfloat16 caches; k_cache and
+// v_cache alike.  The output has q's dtype.
 int cache_format(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache) {
-  TORCH_CHECK(q.scalar_type() == at::kHalf, "pa_decode: q must be float16");
   const at::ScalarType kt = k_cache.scalar_type();
   TORCH_CHECK(v_cache.scalar_type() == kt, "pa_decode: k_cache and v_cache must have the same dtype");
+  if (q.scalar_type() == at::kBFloat16) {
+    TORCH_CHECK(kt == at::kBFloat16, "pa_decode: bfloat16 q needs bfloat16 k_cache and v_cache");
+    return PAD_KV_BF16;
+  }
+  TORCH_CHECK(q.scalar_type() == at::kHalf, "pa_decode: q must be float16 or bfloat16");
   if (kt == at::kHalf) return PAD_KV_FP16;
   if (kt == at::kFloat8_e4m3fn) return PAD_KV_FP8_E4M3FN;
   if (kt == at::kFloat8_e5m2) return PAD_KV_FP8_E5M2;
-  TORCH_CHECK(false, "pa_decode: k_cache and v_cache must be float16, float8_e4m3fn or float8_e5m2");
+  TORCH_CHECK(false, "pa_decode: with float16 q, k_cache and v_cache must be float16, float8_e4m3fn or float8_e5m2");
   return PAD_KV_FP16;
-}
-
-// Checks of the CSR entries: q, caches and the (indptr, indices,
-// last_page_len) triple on one GPU, int32, contiguous, sized by q's batch.
-void check_csr(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache,
-               const torch::Tensor& indptr, const torch::Tensor& indices, const torch::Tensor& last_page_len) {
-  TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && indptr.is_cuda() && indices.is_cuda() &&
-                  last_page_len.is_cuda(),
-              "pa_decode: all tensors must be on the GPU");
-  TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() && q.device() == indptr.device() &&
-                  q.device() == indices.device() && q.device() == last_page_len.device(),
-              "pa_decode: all tensors must be on the same device");
-  TORCH_CHECK(indptr.scalar_type() == at::kInt && indices.scalar_type() == at::kInt &&
-                  last_page_len.scalar_type() == at::kInt,
-              "pa_decode: indptr, indices and last_page_len must be int32");
-  TORCH_CHECK(q.dim() == 3, "pa_decode: q must be [batch, num_q_heads, head_dim]");
-  TORCH_CHECK(k_cache.dim() == 4, "pa_decode: k_cache must be [num_pages, page_size, num_kv_heads, head_dim]");
-  TORCH_CHECK(v_cache.sizes() == k_cache.sizes(), "pa_decode: v_cache shape must match k_cache");
-  TORCH_CHECK(indptr.dim() == 1 && indptr.size(0) == q.size(0) + 1, "pa_decode: indptr must be [batch + 1]");
-  TORCH_CHECK(last_page_len.dim() == 1 && last_page_len.size(0) == q.size(0),
-              "pa_decode: last_page_len must be [batch]");
-  TORCH_CHECK(indices.dim() == 1 && indices.is_contiguous() && indptr.is_contiguous() &&
-                  last_page_len.is_contiguous(),
-              "pa_decode: indptr, indices and last_page_len must be contiguous 1-D tensors");
-  TORCH_CHECK(indices.size(0) <= INT32_MAX, "pa_decode: too many page ids");
-  TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
-}
-
-void check_worklist(const torch::Tensor& q, const torch::Tensor& worklist) {
-  TORCH_CHECK(worklist.is_cuda() && worklist.device() == q.device() && worklist.scalar_type() == at::kByte &&
-                  worklist.is_contiguous(),
-              "pa_decode: worklist must be a contiguous uint8 tensor on q's device");
 }
 
 // The page index of one launch: dense (block_table, seq_lens) or CSR
@@ -341,6 +239,111 @@ torch::Tensor launch_call(const torch::Tensor& q, const torch::Tensor& k_cache, 
   st = pad_decode_launch_call(&c, &d, stream);
   TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
   return out;
+}
+
+// Decode over a dense block table: float16 (either engine), bfloat16 q and
+// caches (MFMA engine), or float16 q with fp8 caches at unit scales (see
+// forward_kv8 for scales).
+torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                      torch::Tensor block_table, torch::Tensor seq_lens, double scale,
+                      int64_t num_splits, int64_t engine) {
+  const int fmt = cache_format(q, k_cache, v_cache);
+  check_dense(q, k_cache, v_cache, block_table, seq_lens);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+  pad_decode_dims d;
+  fill_dims(q, k_cache, v_cache, block_table, seq_lens, out, &d);
+  if (fmt != PAD_KV_FP16)
+    return launch_call(q, k_cache, v_cache, out, d, dense_index(block_table, seq_lens), torch::Tensor(), scale,
+                       num_splits, engine, fmt, 1.0, 1.0);
+
+  const int cus = cached_cus(q.get_device());
+  pad_decode_plan_t plan;
+  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cus, &plan);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  void* ws_ptr = nullptr;
+  int32_t* counters = nullptr;
+  if (!plan.single_pass) {
+    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
+    ws_ptr = sc.workspace.data_ptr();
+    counters = sc.counters.data_ptr<int32_t>();
+  }
+  st = pad_decode_launch_ex(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                            block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
+                            ws_ptr, plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
+                            static_cast<int>(num_splits), static_cast<int>(engine), nullptr, stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return out;
+}
+
+// Decode over fp8 caches (torch.float8_e4m3fn or torch.float8_e5m2, both
+// caches the same) holding K / k_scale and V / v_scale; q and the output
+// stay fp16.  Same plan, scratch and stream as forward().
+torch::Tensor forward_kv8(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
+                          torch::Tensor block_table, torch::Tensor seq_lens, double scale, double k_scale,
+                          double v_scale, int64_t num_splits) {
+  const at::ScalarType kt = k_cache.scalar_type();
+  TORCH_CHECK(kt == at::kFloat8_e4m3fn || kt == at::kFloat8_e5m2,
+              "pa_decode: forward_kv8 needs float8_e4m3fn or float8_e5m2 caches");
+  const int fmt = cache_format(q, k_cache, v_cache);
+  check_dense(q, k_cache, v_cache, block_table, seq_lens);
+  c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
+  pad_decode_dims d;
+  fill_dims(q, k_cache, v_cache, block_table, seq_lens, out, &d);
+
+  const int cus = cached_cus(q.get_device());
+  pad_decode_plan_t plan;
+  int st = pad_decode_plan(&d, static_cast<int>(num_splits), cus, &plan);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  hipStream_t stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.get_device()).stream();
+  void* ws_ptr = nullptr;
+  int32_t* counters = nullptr;
+  if (!plan.single_pass) {
+    StreamScratch& sc = stream_scratch(q, stream, plan.workspace_bytes, plan.counters);
+    ws_ptr = sc.workspace.data_ptr();
+    counters = sc.counters.data_ptr<int32_t>();
+  }
+  st = pad_decode_launch_kv8(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                             block_table.data_ptr<int32_t>(), seq_lens.data_ptr<int32_t>(), out.data_ptr(),
+                             ws_ptr, plan.workspace_bytes, counters, plan.counters, &d, static_cast<float>(scale),
+                             fmt, static_cast<float>(k_scale), static_cast<float>(v_scale),
+                             static_cast<int>(num_splits), stream);
+  TORCH_CHECK(st == PAD_OK, "pa_decode: ", pad_status_string(st));
+  return out;
+}
+
+// Checks of the CSR entries: q, caches and the (indptr, indices,
+// last_page_len) triple on one GPU, int32, contiguous, sized by q's batch.
+void check_csr(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache,
+               const torch::Tensor& indptr, const torch::Tensor& indices, const torch::Tensor& last_page_len) {
+  TORCH_CHECK(q.is_cuda() && k_cache.is_cuda() && v_cache.is_cuda() && indptr.is_cuda() && indices.is_cuda() &&
+                  last_page_len.is_cuda(),
+              "pa_decode: all tensors must be on the GPU");
+  TORCH_CHECK(q.device() == k_cache.device() && q.device() == v_cache.device() && q.device() == indptr.device() &&
+                  q.device() == indices.device() && q.device() == last_page_len.device(),
+              "pa_decode: all tensors must be on the same device");
+  TORCH_CHECK(indptr.scalar_type() == at::kInt && indices.scalar_type() == at::kInt &&
+                  last_page_len.scalar_type() == at::kInt,
+              "pa_decode: indptr, indices and last_page_len must be int32");
+  TORCH_CHECK(q.dim() == 3, "pa_decode: q must be [batch, num_q_heads, head_dim]");
+  TORCH_CHECK(k_cache.dim() == 4, "pa_decode: k_cache must be [num_pages, page_size, num_kv_heads, head_dim]");
+  TORCH_CHECK(v_cache.sizes() == k_cache.sizes(), "pa_decode: v_cache shape must match k_cache");
+  TORCH_CHECK(indptr.dim() == 1 && indptr.size(0) == q.size(0) + 1, "pa_decode: indptr must be [batch + 1]");
+  TORCH_CHECK(last_page_len.dim() == 1 && last_page_len.size(0) == q.size(0),
+              "pa_decode: last_page_len must be [batch]");
+  TORCH_CHECK(indices.dim() == 1 && indices.is_contiguous() && indptr.is_contiguous() &&
+                  last_page_len.is_contiguous(),
+              "pa_decode: indptr, indices and last_page_len must be contiguous 1-D tensors");
+  TORCH_CHECK(indices.size(0) <= INT32_MAX, "pa_decode: too many page ids");
+  TORCH_CHECK(k_cache.size(3) == q.size(2), "pa_decode: q head_dim must match the KV cache head_dim");
+}
+
+void check_worklist(const torch::Tensor& q, const torch::Tensor& worklist) {
+  TORCH_CHECK(worklist.is_cuda() && worklist.device() == q.device() && worklist.scalar_type() == at::kByte &&
+                  worklist.is_contiguous(),
+              "pa_decode: worklist must be a contiguous uint8 tensor on q's device");
 }
 
 // Decode with a CSR page index: the page ids of sequence b are
@@ -455,7 +458,7 @@ torch::Tensor forward_worklist(torch::Tensor q, torch::Tensor k_cache, torch::Te
                                double scale, int64_t num_splits, double k_scale, double v_scale) {
   check_worklist(q, worklist);
   const int fmt = cache_format(q, k_cache, v_cache);
-  check_dense(q, k_cache, v_cache, block_table, seq_lens, k_cache.scalar_type());
+  check_dense(q, k_cache, v_cache, block_table, seq_lens);
   c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
   auto out = torch::empty({q.size(0), q.size(1), q.size(2)}, q.options());
   pad_decode_dims d;

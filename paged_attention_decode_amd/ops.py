@@ -36,11 +36,12 @@ ENGINE_MFMA = 0
 ENGINE_VALU = 1
 
 
-def _check(q, k_cache, v_cache, block_table, seq_lens):
+def _check(q, k_cache, v_cache, block_table, seq_lens, dtypes=(torch.float16,)):
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "paged_attention_decode requires GPU tensors"
     assert block_table.is_cuda and seq_lens.is_cuda, "block_table and seq_lens must be GPU tensors"
-    assert q.dtype == torch.float16 and k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16, (
-        "paged_attention_decode expects fp16 q/k_cache/v_cache"
+    assert q.dtype in dtypes and k_cache.dtype == q.dtype and v_cache.dtype == q.dtype, (
+        "paged_attention_decode expects fp16 q/k_cache/v_cache" if dtypes == (torch.float16,)
+        else f"q, k_cache and v_cache must share one dtype of {dtypes}"
     )
     assert q.dim() == 3 and k_cache.dim() == 4 and v_cache.shape == k_cache.shape, "bad q / cache shapes"
     batch, num_q_heads, head_dim = q.shape
@@ -66,8 +67,12 @@ def _aligned_q(q):
 
 def paged_attention_decode_ex(q, k_cache, v_cache, block_table, seq_lens, num_splits=None, scale=None,
                               engine: int = ENGINE_MFMA):
-    """``paged_attention_decode`` with the phase-1 engine selectable (0 MFMA, 1 VALU/DPP)."""
-    head_dim = _check(q, k_cache, v_cache, block_table, seq_lens)
+    """``paged_attention_decode`` with the phase-1 engine selectable (0 MFMA, 1 VALU/DPP), and bfloat16 too.
+
+    q, k_cache and v_cache are all fp16, or all bfloat16 (MFMA engine; the
+    output is then bfloat16 and P is rounded to bf16 for the PV product)."""
+    head_dim = _check(q, k_cache, v_cache, block_table, seq_lens, (torch.float16, torch.bfloat16))
+    assert q.dtype == torch.float16 or engine == ENGINE_MFMA, "bfloat16 runs on the MFMA engine"
     if num_splits is None:
         num_splits = 0
     else:
@@ -82,7 +87,11 @@ def paged_attention_decode_ex(q, k_cache, v_cache, block_table, seq_lens, num_sp
 
 
 def paged_attention_decode(q, k_cache, v_cache, block_table, seq_lens, num_splits=None, scale=None):
-    """Paged-attention decode on the GPU (drop-in for src/kernel_cuda_v4.py:19-65)."""
+    """Paged-attention decode on the GPU (drop-in for src/kernel_cuda_v4.py:19-65).
+
+    fp16 only, as the reference asserts (src/kernel_cuda_v4.py:37-48);
+    :func:`paged_attention_decode_ex` also takes bfloat16."""
+    _check(q, k_cache, v_cache, block_table, seq_lens)
     return paged_attention_decode_ex(q, k_cache, v_cache, block_table, seq_lens, num_splits, scale)
 
 
@@ -91,33 +100,45 @@ paged_attention_decode_cuda_v4 = paged_attention_decode
 
 FP8_CACHE_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
 FP8_HEAD_DIMS = (64, 128, 256)
-# PAD_KV_* codes of include/pa_decode.h by cache dtype.
-_KV_FORMATS = {torch.float16: 0, torch.float8_e4m3fn: 1, torch.float8_e5m2: 2}
+# PAD_KV_* codes of include/pa_decode.h by cache dtype (bfloat16: q, caches and output).
+_KV_FORMATS = {torch.float16: 0, torch.float8_e4m3fn: 1, torch.float8_e5m2: 2, torch.bfloat16: 3}
 _KV_NAMES = {"float16": torch.float16, "fp16": torch.float16, "half": torch.float16,
+             "bfloat16": torch.bfloat16, "bf16": torch.bfloat16,
              "float8_e4m3fn": torch.float8_e4m3fn, "e4m3fn": torch.float8_e4m3fn, "e4m3": torch.float8_e4m3fn,
              "float8_e5m2": torch.float8_e5m2, "e5m2": torch.float8_e5m2}
 
 
-def _kv_dtype(kv_data_type):
-    """A cache dtype given as a torch dtype or a name (None: float16)."""
+def _kv_dtype(kv_data_type, default=torch.float16):
+    """A dtype given as a torch dtype or a name (None: ``default``)."""
     if kv_data_type is None:
-        return torch.float16
+        return default
     if isinstance(kv_data_type, str):
-        assert kv_data_type in _KV_NAMES, f"unknown kv_data_type {kv_data_type!r}"
+        assert kv_data_type in _KV_NAMES, f"unknown data type {kv_data_type!r}"
         return _KV_NAMES[kv_data_type]
-    assert kv_data_type in _KV_FORMATS, f"kv_data_type must be one of {tuple(_KV_FORMATS)}"
+    assert kv_data_type in _KV_FORMATS, f"data type must be one of {tuple(_KV_FORMATS)}"
     return kv_data_type
 
 
-def _cache_format(k_cache, v_cache, head_dim, engine, k_scale, v_scale):
-    """(PAD_KV_* code, k_scale, v_scale) of the caches; fp8 needs the MFMA engine and head_dim 64/128/256."""
+def _pair_ok(q_dtype, kv_dtype):
+    """fp16 q with fp16 or fp8 caches, or bfloat16 q with bfloat16 caches."""
+    if q_dtype == torch.bfloat16:
+        return kv_dtype == torch.bfloat16
+    return q_dtype == torch.float16 and kv_dtype != torch.bfloat16
+
+
+def _cache_format(q, k_cache, v_cache, head_dim, engine, k_scale, v_scale):
+    """(PAD_KV_* code, k_scale, v_scale) of a call; fp8 and bf16 need the MFMA engine, fp8 head_dim 64/128/256."""
     assert k_cache.dtype in _KV_FORMATS and v_cache.dtype == k_cache.dtype, (
-        "k_cache and v_cache must both be float16, both float8_e4m3fn or both float8_e5m2"
+        "k_cache and v_cache must both be float16, bfloat16, float8_e4m3fn or float8_e5m2"
+    )
+    assert _pair_ok(q.dtype, k_cache.dtype), (
+        "q must be float16 (with float16 or fp8 caches) or bfloat16 (with bfloat16 caches)"
     )
     fmt = _KV_FORMATS[k_cache.dtype]
-    if fmt == 0:
+    if fmt in (0, 3):
         assert k_scale in (None, 1.0) and v_scale in (None, 1.0), "k_scale / v_scale apply to fp8 caches only"
-        return 0, 1.0, 1.0
+        assert fmt == 0 or engine == ENGINE_MFMA, "bfloat16 runs on the MFMA engine"
+        return fmt, 1.0, 1.0
     assert head_dim in FP8_HEAD_DIMS, f"fp8 caches: head_dim must be one of {FP8_HEAD_DIMS}"
     assert engine == ENGINE_MFMA, "fp8 caches run on the MFMA engine"
     k_scale = 1.0 if k_scale is None else float(k_scale)
@@ -221,7 +242,7 @@ def paged_attention_decode_csr(q, k_cache, v_cache, indptr, indices, last_page_l
     """
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "paged_attention_decode requires GPU tensors"
     assert indptr.is_cuda and indices.is_cuda and last_page_len.is_cuda, "CSR index tensors must be GPU tensors"
-    assert q.dtype == torch.float16, "paged_attention_decode expects fp16 q"
+    assert q.dtype in (torch.float16, torch.bfloat16), "paged_attention_decode expects fp16 or bf16 q"
     assert q.dim() == 3 and k_cache.dim() == 4 and v_cache.shape == k_cache.shape, "bad q / cache shapes"
     batch, num_q_heads, head_dim = q.shape
     num_kv_heads = k_cache.shape[2]
@@ -241,7 +262,7 @@ def paged_attention_decode_csr(q, k_cache, v_cache, indptr, indices, last_page_l
     indptr = indptr.to(torch.int32).contiguous()
     indices = indices.to(torch.int32).contiguous()
     last_page_len = last_page_len.to(torch.int32).contiguous()
-    _, k_scale, v_scale = _cache_format(k_cache, v_cache, head_dim, engine, k_scale, v_scale)
+    _, k_scale, v_scale = _cache_format(q, k_cache, v_cache, head_dim, engine, k_scale, v_scale)
     scale = float(scale) if scale is not None else 1.0 / math.sqrt(head_dim)
     return ext().forward_csr(_aligned_q(q), k_cache, v_cache, indptr, indices, last_page_len, scale, num_splits,
                              int(engine), k_scale, v_scale)
@@ -276,24 +297,28 @@ class BatchDecodeWrapper:
     (in a decoding loop, once per step, before the first layer).  The index
     tensors given to ``plan()`` are kept and read again by every ``run()``.
 
+    Data types, with FlashInfer's argument names: ``q_data_type`` (float16
+    by default, or bfloat16) and ``kv_data_type`` (q's type by default).
     fp8 caches: plan with ``kv_data_type=torch.float8_e4m3fn`` (or
-    ``torch.float8_e5m2``, or their names) and pass ``k_scale`` / ``v_scale``
-    to ``run()``, as FlashInfer's wrapper takes them; the result equals
+    ``torch.float8_e5m2``, or their names; q float16) and pass ``k_scale`` /
+    ``v_scale`` to ``run()``; the result equals
     :func:`paged_attention_decode_fp8` (or the CSR call) on the same inputs.
+    bfloat16: ``q_data_type=torch.bfloat16``; q, caches and output bfloat16.
     """
 
     def __init__(self):
         self._plan = None
 
     def plan(self, indptr, indices, last_page_len, num_qo_heads, num_kv_heads, head_dim, page_size,
-             sm_scale=None, num_splits=None, kv_data_type=None):
+             sm_scale=None, num_splits=None, kv_data_type=None, q_data_type=None):
         """Plan over a CSR page index (FlashInfer's layout, see :func:`paged_kv_indices`)."""
         assert indptr.is_cuda and indices.is_cuda and last_page_len.is_cuda, "CSR index tensors must be GPU tensors"
         assert indptr.dim() == 1 and last_page_len.dim() == 1 and indptr.shape[0] == last_page_len.shape[0] + 1, (
             "indptr must be [batch + 1] and last_page_len [batch]"
         )
         assert indices.dim() == 1, "indices must be 1-D"
-        kv_dtype = self._check_geometry(num_qo_heads, num_kv_heads, head_dim, page_size, kv_data_type)
+        q_dtype, kv_dtype = self._check_geometry(num_qo_heads, num_kv_heads, head_dim, page_size, kv_data_type,
+                                                 q_data_type)
         indptr = indptr.to(torch.int32).contiguous()
         indices = indices.to(torch.int32).contiguous()
         last_page_len = last_page_len.to(torch.int32).contiguous()
@@ -302,16 +327,17 @@ class BatchDecodeWrapper:
                                      page_size, splits, _KV_FORMATS[kv_dtype])
         self._plan = ("csr", (indptr, indices, last_page_len), wl, splits,
                       (int(last_page_len.shape[0]), num_qo_heads, num_kv_heads, head_dim, page_size),
-                      self._scale(sm_scale, head_dim), kv_dtype)
+                      self._scale(sm_scale, head_dim), q_dtype, kv_dtype)
 
     def plan_block_table(self, block_table, seq_lens, num_qo_heads, num_kv_heads, head_dim, page_size,
-                         sm_scale=None, num_splits=None, kv_data_type=None):
+                         sm_scale=None, num_splits=None, kv_data_type=None, q_data_type=None):
         """Plan over the reference's dense ``block_table [B, max_pages]`` and ``seq_lens [B]``."""
         assert block_table.is_cuda and seq_lens.is_cuda, "block_table and seq_lens must be GPU tensors"
         assert block_table.dim() == 2 and seq_lens.dim() == 1 and block_table.shape[0] == seq_lens.shape[0], (
             "block_table must be [batch, max_pages] and seq_lens [batch]"
         )
-        kv_dtype = self._check_geometry(num_qo_heads, num_kv_heads, head_dim, page_size, kv_data_type)
+        q_dtype, kv_dtype = self._check_geometry(num_qo_heads, num_kv_heads, head_dim, page_size, kv_data_type,
+                                                 q_data_type)
         if block_table.dtype != torch.int32:
             block_table = block_table.to(torch.int32)
         if seq_lens.dtype != torch.int32:
@@ -321,18 +347,18 @@ class BatchDecodeWrapper:
                                  _KV_FORMATS[kv_dtype])
         self._plan = ("dense", (block_table, seq_lens), wl, splits,
                       (int(seq_lens.shape[0]), num_qo_heads, num_kv_heads, head_dim, page_size),
-                      self._scale(sm_scale, head_dim), kv_dtype)
+                      self._scale(sm_scale, head_dim), q_dtype, kv_dtype)
 
     def run(self, q, paged_kv_cache, k_scale=None, v_scale=None):
-        """Decode ``q [batch, num_qo_heads, head_dim]`` against ``(k_cache, v_cache)``; fp16 shaped like q.
+        """Decode ``q [batch, num_qo_heads, head_dim]`` against ``(k_cache, v_cache)``; q's dtype, shaped like q.
 
         ``k_scale`` / ``v_scale``: the per-tensor scales of fp8 caches (the
         caches hold K / k_scale and V / v_scale)."""
         assert self._plan is not None, "call plan() or plan_block_table() before run()"
-        kind, index, wl, splits, geometry, scale, kv_dtype = self._plan
+        kind, index, wl, splits, geometry, scale, q_dtype, kv_dtype = self._plan
         k_cache, v_cache = paged_kv_cache
         assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "paged_attention_decode requires GPU tensors"
-        assert q.dtype == torch.float16, "paged_attention_decode expects fp16 q"
+        assert q.dtype == q_dtype, f"q must be {q_dtype}, the q_data_type the plan was made for"
         assert k_cache.dtype == kv_dtype and v_cache.dtype == kv_dtype, (
             f"the caches must be {kv_dtype}, the kv_data_type the plan was made for"
         )
@@ -343,24 +369,28 @@ class BatchDecodeWrapper:
             "k_cache does not match the planned page size / heads / head_dim"
         )
         assert k_cache.stride(3) == 1 and v_cache.stride(3) == 1, "K/V caches need a contiguous head_dim"
-        _, k_scale, v_scale = _cache_format(k_cache, v_cache, head_dim, ENGINE_MFMA, k_scale, v_scale)
+        _, k_scale, v_scale = _cache_format(q, k_cache, v_cache, head_dim, ENGINE_MFMA, k_scale, v_scale)
         if kind == "csr":
             return ext().forward_worklist_csr(_aligned_q(q), k_cache, v_cache, *index, wl, scale, splits, k_scale,
                                               v_scale)
         return ext().forward_worklist(_aligned_q(q), k_cache, v_cache, *index, wl, scale, splits, k_scale, v_scale)
 
     @staticmethod
-    def _check_geometry(num_qo_heads, num_kv_heads, head_dim, page_size, kv_data_type=None):
+    def _check_geometry(num_qo_heads, num_kv_heads, head_dim, page_size, kv_data_type=None, q_data_type=None):
         assert num_kv_heads > 0 and num_qo_heads % num_kv_heads == 0, (
             "num_qo_heads must be divisible by num_kv_heads (GQA)"
         )
         assert num_qo_heads // num_kv_heads <= MAX_GQA, f"GQA group larger than {MAX_GQA}"
         assert head_dim in SUPPORTED_HEAD_DIMS, f"head_dim must be one of {SUPPORTED_HEAD_DIMS}"
         assert page_size >= 1, "page_size must be >= 1"
-        kv_dtype = _kv_dtype(kv_data_type)
-        if kv_dtype != torch.float16:
+        q_dtype = _kv_dtype(q_data_type)
+        kv_dtype = _kv_dtype(kv_data_type, q_dtype)
+        assert _pair_ok(q_dtype, kv_dtype), (
+            "q_data_type float16 (with float16 or fp8 caches) or bfloat16 (with bfloat16 caches)"
+        )
+        if kv_dtype in FP8_CACHE_DTYPES:
             assert head_dim in FP8_HEAD_DIMS, f"fp8 caches: head_dim must be one of {FP8_HEAD_DIMS}"
-        return kv_dtype
+        return q_dtype, kv_dtype
 
     @staticmethod
     def _splits(num_splits):

@@ -14,7 +14,9 @@ one set of inputs with ``--warm``.  Prints the per-call algorithmic bytes.
 
 ``--kv e4m3fn`` (or ``e5m2``) converts every input set's caches to fp8
 (workloads.to_fp8) and calls ``paged_attention_decode_fp8``; the printed
-algorithmic bytes then count one byte per K/V element.
+algorithmic bytes then count one byte per K/V element.  ``--kv bf16``
+rounds q and the caches to bfloat16 (workloads.to_bf16) and calls
+``paged_attention_decode_ex``.
 
 ``--planned`` plans every input set once with ``BatchDecodeWrapper``
 (the work-list planner kernel, one dispatch per set, before the timed
@@ -86,7 +88,7 @@ def main() -> None:
     p.add_argument("--configs", default="C2:16,C2:32,C2:64,C3,C4", help="--timeline: configurations")
     p.add_argument("--repeats", type=int, default=8, help="--timeline: groups of 4 launches")
     p.add_argument("--json", default="", help="--timeline: write the table here")
-    p.add_argument("--kv", default="fp16", choices=["fp16", "e4m3fn", "e5m2"], help="K/V cache format")
+    p.add_argument("--kv", default="fp16", choices=["fp16", "bf16", "e4m3fn", "e5m2"], help="q/K/V format")
     p.add_argument("--planned", action="store_true",
                    help="plan every input set once (BatchDecodeWrapper), then time only run() calls")
     a = p.parse_args()
@@ -120,6 +122,8 @@ def main() -> None:
         make16 = make
 
         def make(seed):
+            if a.kv == "bf16":
+                return wl.to_bf16(make16(seed))
             return wl.to_fp8(make16(seed), wl.FP8_NAMES[a.kv])
     sets = _sets(make, a.warm)
     w0, n_sets = sets[0], len(sets)
@@ -138,7 +142,7 @@ def main() -> None:
         w = sets[i % n_sets]
         if a.planned:
             wraps[i % n_sets].run(w.q, (w.k_cache, w.v_cache))
-        elif a.kv != "fp16":
+        elif a.kv in ("e4m3fn", "e5m2"):
             paged_attention_decode_fp8(*w.args(), k_scale=w.k_scale, v_scale=w.v_scale,
                                        num_splits=a.num_splits or None)
         else:

@@ -18,7 +18,8 @@ and within sequences; unused block_table columns point at valid pages):
 valid token, the q read and the output write, the block_table entries of the
 used pages and seq_lens (the split workspace is excluded as overhead).
 
-``to_fp8`` turns a workload's caches into fp8 codes (float8_e4m3fn or
+``to_bf16`` rounds q and the caches to bfloat16.  ``to_fp8`` turns a
+workload's caches into fp8 codes (float8_e4m3fn or
 float8_e5m2) of K / k_scale and V / v_scale, per-tensor scales chosen so the
 largest magnitude lands at 7/8 of the format's range; its algorithmic bytes
 count one byte per K/V element.
@@ -164,3 +165,9 @@ def to_fp8(w: Workload, dtype=torch.float8_e4m3fn) -> Workload:
     v8, vs = quant(w.v_cache)
     name = w.name + "_" + next(n for n, t in FP8_NAMES.items() if t == dtype)
     return Workload(name, w.q, k8, v8, w.block_table, w.seq_lens, list(w.seq_lens_host), w.scale, ks, vs)
+
+
+def to_bf16(w: Workload) -> Workload:
+    """The same workload in bfloat16 (q and both caches rounded)."""
+    return Workload(w.name + "_bf16", w.q.bfloat16(), w.k_cache.bfloat16(), w.v_cache.bfloat16(), w.block_table,
+                    w.seq_lens, list(w.seq_lens_host), w.scale)
