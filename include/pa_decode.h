@@ -90,14 +90,17 @@ typedef enum pad_status {
                                     positive                                */
 } pad_status;
 
-/* Element formats of the K/V caches (pad_decode_launch_kv8,
- * pad_decode_launch_call).  fp8 caches pair with fp16 q and out. */
+/* Data formats of a call (pad_decode_launch_kv8, pad_decode_launch_call):
+ * the caches' element type and, for fp8 caches, whether q and out are fp16
+ * (PAD_KV_FP8_E4M3FN / _E5M2) or bfloat16 (..._BF16). */
 #define PAD_KV_FP16 0         /* IEEE half (every other entry point)          */
 #define PAD_KV_FP8_E4M3FN 1   /* OCP fp8 E4M3 "fn": bias 7, no infinities     */
 #define PAD_KV_FP8_E5M2 2     /* OCP fp8 E5M2: bias 15, IEEE-like             */
 #define PAD_KV_BF16 3         /* bfloat16 q, caches and out (pad_decode_launch_call;
                                  MFMA engine, every head_dim; P is rounded to
                                  bf16 for the PV product)                     */
+#define PAD_KV_FP8_E4M3FN_BF16 4  /* e4m3fn caches with bfloat16 q and out    */
+#define PAD_KV_FP8_E5M2_BF16 5    /* e5m2 caches with bfloat16 q and out       */
 
 /* Static scratch of pad_decode_launch_noalloc(), per device: fp32 partials
  * and int32 arrival counters.  48 MiB in all, held until the process ends. */
@@ -225,13 +228,14 @@ int pad_decode_launch(const void* q, const void* k_cache, const void* v_cache,
                       int num_splits, void* stream);
 
 /* pad_decode_launch() over fp8 K/V caches: k_cache / v_cache hold one byte
- * per element in `kv_format` (PAD_KV_FP8_E4M3FN or PAD_KV_FP8_E5M2; the
+ * per element in `kv_format` (PAD_KV_FP8_E4M3FN or PAD_KV_FP8_E5M2 with fp16
+ * q and out, PAD_KV_FP8_E4M3FN_BF16 or PAD_KV_FP8_E5M2_BF16 with bfloat16; the
  * layouts, strides in elements = bytes, of the fp16 caches), and represent
  * K = k_scale * k_cache and V = v_scale * v_cache (per-tensor scales, the
- * convention of serving engines' fp8 KV caches).  q and out stay fp16;
- * head_dim 64, 128 or 256.  Each element is widened to fp16 exactly in
- * registers, so the result equals the fp16 path's on the dequantized
- * caches up to fp32 rounding: k_scale goes into the softmax scale and
+ * convention of serving engines' fp8 KV caches); head_dim 64, 128 or 256.
+ * Each element is widened exactly in registers to q's format, so the result
+ * equals the fp16 (bfloat16) path's on the dequantized caches up to fp32
+ * rounding: k_scale goes into the softmax scale and
  * v_scale into the output normalisation.  Same splits, workspace and
  * counters as pad_decode_launch() (pad_decode_plan(),
  * pad_decode_workspace_bytes(), pad_decode_counters_needed()); workgroups

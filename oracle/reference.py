@@ -126,17 +126,19 @@ def decode_bf16_protocol(q, k_cache, v_cache, block_table, seq_lens, scale=None)
                                             seq_lens.detach().to("cpu"), scale)
 
 
-def decode_fp8_protocol(q, k_cache, v_cache, block_table, seq_lens, k_scale=1.0, v_scale=1.0, scale=None):
+def decode_fp8_protocol(q, k_cache, v_cache, block_table, seq_lens, k_scale=1.0, v_scale=1.0, scale=None,
+                        q_dtype=torch.float16):
     """Oracle for fp8 caches: the fp32 oracle on the dequantised caches.
 
     k_cache / v_cache are torch.float8_e4m3fn or torch.float8_e5m2 holding
     K / k_scale and V / v_scale (per-tensor scales); the oracle decodes each
     code with PyTorch's float8 -> float32 conversion, multiplies by the
-    scale in fp32 and runs ``paged_attention_decode_reference`` on fp16-rounded
-    q.  The reference's caches are fp16 only (src/kernel_cuda_v4.py:37-48);
-    this extends its oracle to the dequantised values.
+    scale in fp32 and runs ``paged_attention_decode_reference`` on q rounded
+    to ``q_dtype`` (fp16, or bfloat16 for a bf16 caller).  The reference's
+    caches are fp16 only (src/kernel_cuda_v4.py:37-48); this extends its
+    oracle to the dequantised values.
     """
-    q32 = q.detach().to("cpu").half().float()
+    q32 = q.detach().to("cpu").to(q_dtype).float()
     k32 = k_cache.detach().to("cpu").float() * float(k_scale)
     v32 = v_cache.detach().to("cpu").float() * float(v_scale)
     return paged_attention_decode_reference(q32, k32, v32, block_table.detach().to("cpu"),

@@ -414,20 +414,27 @@ constexpr int kModeSubpage = 2;
 // is the fp16 path; or bfloat16 q, caches and output, which run the same
 // path on bf16 MFMAs (P rounded to bf16, as fp16 P is to fp16).
 constexpr int kKvF16 = 0;
-constexpr int kKvE4M3 = 1;  // float8_e4m3fn caches, fp16 q and output
-constexpr int kKvE5M2 = 2;  // float8_e5m2 caches, fp16 q and output
-constexpr int kKvBF16 = 3;  // bfloat16 q, caches and output
+constexpr int kKvE4M3 = 1;   // float8_e4m3fn caches, fp16 q and output
+constexpr int kKvE5M2 = 2;   // float8_e5m2 caches, fp16 q and output
+constexpr int kKvBF16 = 3;   // bfloat16 q, caches and output
+constexpr int kKvE4M3B = 4;  // float8_e4m3fn caches, bfloat16 q and output
+constexpr int kKvE5M2B = 5;  // float8_e5m2 caches, bfloat16 q and output
 
 template <int KVF>
-constexpr bool kv_is_fp8() { return KVF == kKvE4M3 || KVF == kKvE5M2; }
+constexpr bool kv_is_fp8() { return KVF == kKvE4M3 || KVF == kKvE5M2 || KVF == kKvE4M3B || KVF == kKvE5M2B; }
+template <int KVF>
+constexpr bool kv_is_e4m3() { return KVF == kKvE4M3 || KVF == kKvE4M3B; }
+// bfloat16 q, P and output (and MFMAs); fp16 otherwise.
+template <int KVF>
+constexpr bool q_is_bf16() { return KVF == kKvBF16 || KVF == kKvE4M3B || KVF == kKvE5M2B; }
 template <int KVF>
 constexpr int kv_elem_bytes() { return kv_is_fp8<KVF>() ? 1 : 2; }
 
 // One 16x16x16 MFMA step on 16-bit operands held as fp16 vectors: fp16, or
-// the bit patterns of bfloat16 values (KVF == kKvBF16).
+// the bit patterns of bfloat16 values (q_is_bf16).
 template <int KVF>
 __device__ __forceinline__ f4_t mfma16(h4_t a, h4_t b, f4_t c) {
-  if constexpr (KVF == kKvBF16) {
+  if constexpr (q_is_bf16<KVF>()) {
     typedef short s4_t __attribute__((ext_vector_type(4)));
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4_t, a), __builtin_bit_cast(s4_t, b), c,
                                                      0, 0, 0);
@@ -437,34 +444,49 @@ __device__ __forceinline__ f4_t mfma16(h4_t a, h4_t b, f4_t c) {
 }
 
 // x rounded (to nearest even) to the output format, as 16 bits in an fp16
-// slot: fp16, or bfloat16 for KVF == kKvBF16.
+// slot: fp16, or bfloat16 (q_is_bf16).
 template <int KVF>
 __device__ __forceinline__ _Float16 round16(float x) {
-  if constexpr (KVF == kKvBF16)
+  if constexpr (q_is_bf16<KVF>())
     return __builtin_bit_cast(_Float16, (__bf16)x);
   else
     return (_Float16)x;
 }
 
-// Four fp8 codes (one dword, element i in byte i) as four fp16 values (two
-// dwords: elements 0-1 in lo, 2-3 in hi) with gfx950's scaled conversions
-// (v_cvt_scalef32_pk_f16_fp8 / _bf8, one per pair).  Their scale operand
-// acts through its exponent only, so it is 1 here and the launch folds the
+// Four fp8 codes (one dword, element i in byte i) as four 16-bit values
+// (two dwords: elements 0-1 in lo, 2-3 in hi) in the compute format, fp16
+// or bfloat16, with gfx950's scaled conversions (v_cvt_scalef32_pk_f16_fp8 /
+// _bf8, or _pk_bf16_fp8 / _bf8, one per pair).  Their scale operand acts
+// through its exponent only, so it is 1 here and the launch folds the
 // caller's k_scale / v_scale into the softmax scale and the output
-// normalisation.  At scale 1 every code converts exactly, NaN codes to fp16
-// NaNs (every e4m3fn value and every e5m2 value is an fp16 value).
+// normalisation.  At scale 1 every code converts exactly, NaN codes to NaNs
+// (every e4m3fn value and every e5m2 value is an fp16 and a bf16 value).
 template <int KVF>
-__device__ __forceinline__ void fp8x4_to_f16x4(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  h2_t a, b;
-  if constexpr (KVF == kKvE4M3) {
-    a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
-    b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true);
+__device__ __forceinline__ void fp8x4_to_16x4(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  if constexpr (q_is_bf16<KVF>()) {
+    typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+    b2_t a, b;
+    if constexpr (kv_is_e4m3<KVF>()) {
+      a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+      b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+    } else {
+      a = __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, false);
+      b = __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w, 1.0f, true);
+    }
+    lo = __builtin_bit_cast(uint32_t, a);
+    hi = __builtin_bit_cast(uint32_t, b);
   } else {
-    a = __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, false);
-    b = __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, true);
+    h2_t a, b;
+    if constexpr (kv_is_e4m3<KVF>()) {
+      a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
+      b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true);
+    } else {
+      a = __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, false);
+      b = __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w, 1.0f, true);
+    }
+    lo = __builtin_bit_cast(uint32_t, a);
+    hi = __builtin_bit_cast(uint32_t, b);
   }
-  lo = __builtin_bit_cast(uint32_t, a);
-  hi = __builtin_bit_cast(uint32_t, b);
 }
 
 // head_dim 256 keeps the Q^T operand in LDS instead of 32 VGPRs per lane
@@ -528,7 +550,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
     } else {
       HVec<NDW> r;
 #pragma unroll
-      for (int w = 0; w < NDWR; ++w) fp8x4_to_f16x4<KVF>(x.w[w], r.w[2 * w], r.w[2 * w + 1]);
+      for (int w = 0; w < NDWR; ++w) fp8x4_to_16x4<KVF>(x.w[w], r.w[2 * w], r.w[2 * w + 1]);
       return r;
     }
   };
@@ -748,7 +770,7 @@ __device__ __forceinline__ void wave_loop_mfma(const Phase1Args& a, int phys_fir
     }
     h4_t ph;
     float psum = 0.f;  // l accumulates the same rounded weights P.V uses
-    if constexpr (KVF == kKvBF16) {
+    if constexpr (q_is_bf16<KVF>()) {
       // Pairs through the packed conversion; a rounded bf16 pair's floats
       // are its high and low halves shifted into place.
       typedef float f2_t __attribute__((ext_vector_type(2)));
@@ -1372,7 +1394,8 @@ __device__ __forceinline__ bool worklist_item(const Phase1Args& a, int g, int G,
 // not fit 168 registers without one VGPR spilled to scratch; so do the
 // bfloat16 sub-page modes of head_dim 128 (2 VGPRs spilled at page size 4).
 constexpr int phase1_waves_per_simd(int d, int engine, int mode, int kvf) {
-  const bool wide = d == 128 && (mode == 0 || (kvf == kKvBF16 && mode >= kModeSubpage));
+  const bool wide = d == 128 && (mode == 0 || ((kvf == kKvBF16 || kvf == kKvE4M3B || kvf == kKvE5M2B) &&
+                                                 mode >= kModeSubpage));
   return engine == 0 ? (d <= 128 ? (wide ? 2 : 3) : 1) : 1;
 }
 
@@ -2094,10 +2117,14 @@ static size_t worklist_bytes_for(const pad_decode_plan_t& plan, const pad_decode
 
 // A known format; bfloat16 and fp8 on the MFMA engine; fp8 with head_dim
 // 64/128/256 and finite positive scales (the scales are read for fp8 only).
+static bool kv_format_fp8(int f) {
+  return f == PAD_KV_FP8_E4M3FN || f == PAD_KV_FP8_E5M2 || f == PAD_KV_FP8_E4M3FN_BF16 || f == PAD_KV_FP8_E5M2_BF16;
+}
+
 static int check_kv_format(int kv_format, int engine, const pad_decode_dims* d, float k_scale, float v_scale) {
   if (kv_format == PAD_KV_FP16) return PAD_OK;
   if (kv_format == PAD_KV_BF16) return engine == 0 ? PAD_OK : PAD_ERR_KV_FORMAT;
-  if (kv_format != PAD_KV_FP8_E4M3FN && kv_format != PAD_KV_FP8_E5M2) return PAD_ERR_KV_FORMAT;
+  if (!kv_format_fp8(kv_format)) return PAD_ERR_KV_FORMAT;
   if (engine != 0) return PAD_ERR_KV_FORMAT;
   if (d && d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return PAD_ERR_UNSUPPORTED_HEAD_DIM;
   if (!(k_scale > 0.0f) || !(v_scale > 0.0f) || k_scale > 1.0e30f || v_scale > 1.0e30f) return PAD_ERR_KV_FORMAT;
@@ -2115,7 +2142,7 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
   int st = check_kv_format(kv_format, engine, d, k_scale, v_scale);
   if (st != PAD_OK) return st;
   Launch L;
-  const bool fp8 = kv_format == PAD_KV_FP8_E4M3FN || kv_format == PAD_KV_FP8_E5M2;
+  const bool fp8 = kv_format_fp8(kv_format);
   st = setup_launch(q, k, v, bt, sl, indptr, lpl, out, ws, ws_bytes, counters, num_counters, d, scale,
                     num_splits, engine, true, &L, fp8 ? 1 : 2);
   if (st != PAD_OK || L.empty) return st;
@@ -2142,6 +2169,10 @@ static int launch_impl(const void* q, const void* k, const void* v, const int32_
     e = dispatch_kvf_dim<kKvE5M2>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
   } else if (kv_format == PAD_KV_BF16) {
     e = dispatch_kvf_dim<kKvBF16>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
+  } else if (kv_format == PAD_KV_FP8_E4M3FN_BF16) {
+    e = dispatch_kvf_dim<kKvE4M3B>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
+  } else if (kv_format == PAD_KV_FP8_E5M2_BF16) {
+    e = dispatch_kvf_dim<kKvE5M2B>(L.a, d->head_dim, L.grid, L.nw, L.lds, hs);
   } else switch (d->head_dim) {
     case 32: e = dispatch_phase1<32>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
     case 64: e = dispatch_phase1<64>(L.a, L.grid, L.nw, L.lds, engine, hs); break;
@@ -2303,7 +2334,7 @@ int pad_decode_launch_kv8(const void* q, const void* k_cache, const void* v_cach
                           int32_t* counters, int64_t num_counters, const pad_decode_dims* dims, float scale,
                           int kv_format, float k_scale, float v_scale, int num_splits, void* stream) {
   // fp16 caches: pad_decode_launch; bfloat16: pad_decode_launch_call
-  if (kv_format != PAD_KV_FP8_E4M3FN && kv_format != PAD_KV_FP8_E5M2) return PAD_ERR_KV_FORMAT;
+  if (!pad::kv_format_fp8(kv_format)) return PAD_ERR_KV_FORMAT;
   return pad::launch_impl(q, k_cache, v_cache, block_table, seq_lens, nullptr, nullptr, out, workspace,
                           workspace_bytes, counters, num_counters, dims, scale, num_splits, 0, nullptr, stream,
                           nullptr, 0, kv_format, k_scale, v_scale);
@@ -2378,7 +2409,7 @@ int pad_decode_plan_worklist_call(const pad_decode_call* c, const pad_decode_dim
   if (c->engine != 0) return PAD_ERR_INVALID_SHAPE;  // work lists serve the MFMA engine
   const int st = pad::check_kv_format(c->kv_format, 0, dims, c->k_scale, c->v_scale);
   if (st != PAD_OK) return st;
-  const bool fp8 = c->kv_format == PAD_KV_FP8_E4M3FN || c->kv_format == PAD_KV_FP8_E5M2;
+  const bool fp8 = pad::kv_format_fp8(c->kv_format);
   return pad::plan_worklist_impl(c->block_table, csr ? nullptr : c->seq_lens, c->indptr, c->last_page_len, dims,
                                  c->num_splits, worklist, worklist_bytes, stream, fp8 ? 1 : 2);
 }
@@ -2418,8 +2449,8 @@ const char* pad_status_string(int status) {
       return "the call needs more split scratch than pad_decode_launch_noalloc's static buffer holds "
              "(PAD_NOALLOC_WORKSPACE_BYTES of partials, PAD_NOALLOC_COUNTERS counters); use pad_decode_launch";
     case PAD_ERR_KV_FORMAT:
-      return "unsupported K/V cache format or scale (fp8: PAD_KV_FP8_E4M3FN or PAD_KV_FP8_E5M2, MFMA engine, "
-             "finite positive k_scale and v_scale; PAD_KV_BF16: MFMA engine)";
+      return "unsupported K/V cache format or scale (fp8: PAD_KV_FP8_E4M3FN / _E5M2 (fp16 q) or _BF16 (bfloat16 "
+             "q), MFMA engine, head_dim 64/128/256, finite positive k_scale and v_scale; PAD_KV_BF16: MFMA engine)";
     default: return "unknown status";
   }
 }

@@ -143,14 +143,17 @@ void check_dense(const torch::Tensor& q, const torch::Tensor& k_cache, const tor
 }
 
 // PAD_KV_* format of a call: float16 q with float16 or fp8 (float8_e4m3fn /
-// float8_e5m2) caches, or bfloat16 q with bfloat16 caches; k_cache and
-// v_cache alike.  The output has q's dtype.
+// float8_e5m2) caches, or bfloat16 q with bfloat16 or fp8 caches; k_cache
+// and v_cache alike.  The output has q's dtype.
 int cache_format(const torch::Tensor& q, const torch::Tensor& k_cache, const torch::Tensor& v_cache) {
   const at::ScalarType kt = k_cache.scalar_type();
   TORCH_CHECK(v_cache.scalar_type() == kt, "pa_decode: k_cache and v_cache must have the same dtype");
   if (q.scalar_type() == at::kBFloat16) {
-    TORCH_CHECK(kt == at::kBFloat16, "pa_decode: bfloat16 q needs bfloat16 k_cache and v_cache");
-    return PAD_KV_BF16;
+    if (kt == at::kBFloat16) return PAD_KV_BF16;
+    if (kt == at::kFloat8_e4m3fn) return PAD_KV_FP8_E4M3FN_BF16;
+    if (kt == at::kFloat8_e5m2) return PAD_KV_FP8_E5M2_BF16;
+    TORCH_CHECK(false, "pa_decode: with bfloat16 q, k_cache and v_cache must be bfloat16, float8_e4m3fn or "
+                       "float8_e5m2");
   }
   TORCH_CHECK(q.scalar_type() == at::kHalf, "pa_decode: q must be float16 or bfloat16");
   if (kt == at::kHalf) return PAD_KV_FP16;
@@ -279,7 +282,7 @@ torch::Tensor forward(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_ca
 
 // Decode over fp8 caches (torch.float8_e4m3fn or torch.float8_e5m2, both
 // caches the same) holding K / k_scale and V / v_scale; q and the output
-// stay fp16.  Same plan, scratch and stream as forward().
+// are float16 or bfloat16.  Same plan, scratch and stream as forward().
 torch::Tensor forward_kv8(torch::Tensor q, torch::Tensor k_cache, torch::Tensor v_cache,
                           torch::Tensor block_table, torch::Tensor seq_lens, double scale, double k_scale,
                           double v_scale, int64_t num_splits) {

@@ -120,10 +120,16 @@ def _kv_dtype(kv_data_type, default=torch.float16):
 
 
 def _pair_ok(q_dtype, kv_dtype):
-    """fp16 q with fp16 or fp8 caches, or bfloat16 q with bfloat16 caches."""
+    """fp16 q with fp16 or fp8 caches, or bfloat16 q with bfloat16 or fp8 caches."""
     if q_dtype == torch.bfloat16:
-        return kv_dtype == torch.bfloat16
+        return kv_dtype != torch.float16
     return q_dtype == torch.float16 and kv_dtype != torch.bfloat16
+
+
+def _format_code(q_dtype, kv_dtype):
+    """PAD_KV_* code of a call (fp8 caches with bfloat16 q: the ``_BF16`` codes 4 and 5)."""
+    code = _KV_FORMATS[kv_dtype]
+    return code + 3 if q_dtype == torch.bfloat16 and kv_dtype in FP8_CACHE_DTYPES else code
 
 
 def _cache_format(q, k_cache, v_cache, head_dim, engine, k_scale, v_scale):
@@ -132,9 +138,9 @@ def _cache_format(q, k_cache, v_cache, head_dim, engine, k_scale, v_scale):
         "k_cache and v_cache must both be float16, bfloat16, float8_e4m3fn or float8_e5m2"
     )
     assert _pair_ok(q.dtype, k_cache.dtype), (
-        "q must be float16 (with float16 or fp8 caches) or bfloat16 (with bfloat16 caches)"
+        "q must be float16 (with float16 or fp8 caches) or bfloat16 (with bfloat16 or fp8 caches)"
     )
-    fmt = _KV_FORMATS[k_cache.dtype]
+    fmt = _format_code(q.dtype, k_cache.dtype)
     if fmt in (0, 3):
         assert k_scale in (None, 1.0) and v_scale in (None, 1.0), "k_scale / v_scale apply to fp8 caches only"
         assert fmt == 0 or engine == ENGINE_MFMA, "bfloat16 runs on the MFMA engine"
@@ -157,15 +163,15 @@ def paged_attention_decode_fp8(q, k_cache, v_cache, block_table, seq_lens, k_sca
     ``torch.float8_e5m2`` (both the same), laid out as the fp16 caches
     ``[num_pages, page_size, num_kv_heads, head_dim]``, and hold
     ``K / k_scale`` and ``V / v_scale`` (per-tensor scales, Python floats).
-    The result equals the fp16 operator on the dequantised caches
+    The result equals the fp16 (bfloat16) operator on the dequantised caches
     ``k_cache.float() * k_scale`` and ``v_cache.float() * v_scale``: every fp8
-    code widens to fp16 exactly.  q and the output are fp16; head_dim 64, 128
-    or 256; the MFMA engine only.  No counterpart in the reference, whose
-    caches are fp16 only (src/kernel_cuda_v4.py:37-48).
+    code widens to fp16 and to bf16 exactly.  q and the output are fp16 or
+    bfloat16; head_dim 64, 128 or 256; the MFMA engine only.  No counterpart
+    in the reference, whose caches are fp16 only (src/kernel_cuda_v4.py:37-48).
     """
     assert q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "paged_attention_decode requires GPU tensors"
     assert block_table.is_cuda and seq_lens.is_cuda, "block_table and seq_lens must be GPU tensors"
-    assert q.dtype == torch.float16, "q must be fp16"
+    assert q.dtype in (torch.float16, torch.bfloat16), "q must be fp16 or bf16"
     assert k_cache.dtype in FP8_CACHE_DTYPES and v_cache.dtype == k_cache.dtype, (
         "k_cache and v_cache must both be float8_e4m3fn or both float8_e5m2"
     )
@@ -300,10 +306,11 @@ class BatchDecodeWrapper:
     Data types, with FlashInfer's argument names: ``q_data_type`` (float16
     by default, or bfloat16) and ``kv_data_type`` (q's type by default).
     fp8 caches: plan with ``kv_data_type=torch.float8_e4m3fn`` (or
-    ``torch.float8_e5m2``, or their names; q float16) and pass ``k_scale`` /
-    ``v_scale`` to ``run()``; the result equals
+    ``torch.float8_e5m2``, or their names; q float16 or bfloat16) and pass
+    ``k_scale`` / ``v_scale`` to ``run()``; the result equals
     :func:`paged_attention_decode_fp8` (or the CSR call) on the same inputs.
-    bfloat16: ``q_data_type=torch.bfloat16``; q, caches and output bfloat16.
+    bfloat16: ``q_data_type=torch.bfloat16``; q and output bfloat16, caches
+    bfloat16 unless ``kv_data_type`` names an fp8 type.
     """
 
     def __init__(self):
@@ -324,7 +331,7 @@ class BatchDecodeWrapper:
         last_page_len = last_page_len.to(torch.int32).contiguous()
         splits = self._splits(num_splits)
         wl = ext().plan_worklist_csr(indptr, indices, last_page_len, num_qo_heads, num_kv_heads, head_dim,
-                                     page_size, splits, _KV_FORMATS[kv_dtype])
+                                     page_size, splits, _format_code(q_dtype, kv_dtype))
         self._plan = ("csr", (indptr, indices, last_page_len), wl, splits,
                       (int(last_page_len.shape[0]), num_qo_heads, num_kv_heads, head_dim, page_size),
                       self._scale(sm_scale, head_dim), q_dtype, kv_dtype)
@@ -344,7 +351,7 @@ class BatchDecodeWrapper:
             seq_lens = seq_lens.to(torch.int32)
         splits = self._splits(num_splits)
         wl = ext().plan_worklist(block_table, seq_lens, num_qo_heads, num_kv_heads, head_dim, page_size, splits,
-                                 _KV_FORMATS[kv_dtype])
+                                 _format_code(q_dtype, kv_dtype))
         self._plan = ("dense", (block_table, seq_lens), wl, splits,
                       (int(seq_lens.shape[0]), num_qo_heads, num_kv_heads, head_dim, page_size),
                       self._scale(sm_scale, head_dim), q_dtype, kv_dtype)
@@ -386,7 +393,7 @@ class BatchDecodeWrapper:
         q_dtype = _kv_dtype(q_data_type)
         kv_dtype = _kv_dtype(kv_data_type, q_dtype)
         assert _pair_ok(q_dtype, kv_dtype), (
-            "q_data_type float16 (with float16 or fp8 caches) or bfloat16 (with bfloat16 caches)"
+            "q_data_type float16 (with float16 or fp8 caches) or bfloat16 (with bfloat16 or fp8 caches)"
         )
         if kv_dtype in FP8_CACHE_DTYPES:
             assert head_dim in FP8_HEAD_DIMS, f"fp8 caches: head_dim must be one of {FP8_HEAD_DIMS}"

@@ -35,12 +35,14 @@ FIELDS = {
 
 def _demangle_args(name: str) -> str:
     # _ZN3pad17pad_phase1_kernelILi128ELi1ELi0ELi0ELi0EEEvNS_10Phase1ArgsE -> <128, 1, 0, 0> (fp16 caches);
-    # a fifth argument of 1, 2 or 3 is printed as e4m3fn / e5m2 (fp8 caches) / bf16.
+    # a fifth argument of 1-5 is printed as e4m3fn / e5m2 (fp8 caches, fp16 q),
+    # bf16, e4m3fn/bf16 / e5m2/bf16 (fp8 caches, bfloat16 q).
     args = re.findall(r"Li(\d+)E", name)
     if len(args) == 5:
         kvf = args.pop()
         if kvf != "0":
-            args.append({"1": "e4m3fn", "2": "e5m2", "3": "bf16"}.get(kvf, kvf))
+            args.append({"1": "e4m3fn", "2": "e5m2", "3": "bf16", "4": "e4m3fn/bf16",
+                         "5": "e5m2/bf16"}.get(kvf, kvf))
     return "<" + ", ".join(args) + ">" if args else name
 
 

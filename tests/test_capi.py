@@ -507,8 +507,8 @@ def test_launch_call_checks_on_the_host():
     wl_valu = _native.PadCall.from_buffer_copy(c)
     wl_valu.worklist, wl_valu.worklist_bytes, wl_valu.engine = fake, 1 << 20, 1
     assert lib.pad_decode_launch_call(ctypes.byref(wl_valu), ctypes.byref(dm), None) == 2
-    for fmt, ks, engine, code in ((4, 1.0, 0, 12), (-1, 1.0, 0, 12), (1, 0.0, 0, 12), (1, 1.0, 1, 12),
-                                  (2, float("inf"), 0, 12), (3, 1.0, 1, 12)):
+    for fmt, ks, engine, code in ((6, 1.0, 0, 12), (-1, 1.0, 0, 12), (1, 0.0, 0, 12), (1, 1.0, 1, 12),
+                                  (4, 0.0, 0, 12), (2, float("inf"), 0, 12), (3, 1.0, 1, 12)):
         bad = _native.PadCall.from_buffer_copy(c)
         bad.kv_format, bad.k_scale, bad.engine = fmt, ks, engine
         assert lib.pad_decode_launch_call(ctypes.byref(bad), ctypes.byref(dm), None) == code, (fmt, ks, engine)

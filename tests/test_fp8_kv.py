@@ -442,3 +442,83 @@ def test_fp8_fuzz_matrix(seed):
         torch.cuda.synchronize()
         assert_parity(a.cpu(), expected)
         assert_parity(b.cpu(), expected)
+
+
+# fp8 caches with bfloat16 q and output (PAD_KV_FP8_*_BF16): the codes widen
+# to bf16 exactly, the rest is the bfloat16 path (bf16 MFMAs, P and output
+# rounded to bf16), so the tolerance is the bf16 one, atol = rtol = 1e-2.
+BF16_TOL = 1e-2
+
+
+def _close_bf16(actual, expected):
+    a, e = actual.float().cpu(), expected.float().cpu()
+    assert torch.isfinite(a).all()
+    err = (a - e).abs()
+    assert bool((err <= BF16_TOL + BF16_TOL * e.abs()).all()), err.max().item()
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("ps", [16, 4, 12])
+def test_fp8_caches_with_bf16_q_match_oracle(fmt, d, ps):
+    import paged_attention_decode_amd as pad
+
+    lens = [1, ps + 3, 150, 777, 0]
+    q, k, v, bt, sl = _case(lens, ps, 2, 6, d, seed=ps + d + 500)
+    ks, vs = float(k.abs().max()) / 300.0, float(v.abs().max()) / 111.0
+    k8, v8 = _quant(k, fmt, ks), _quant(v, fmt, vs)
+    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs, q_dtype=torch.bfloat16)
+    qd = q.bfloat16().cuda()
+    for splits in (None, 1, 5):
+        out = pad.paged_attention_decode_fp8(qd, k8.cuda(), v8.cuda(), bt.cuda(), sl.cuda(), k_scale=ks,
+                                             v_scale=vs, num_splits=splits)
+        torch.cuda.synchronize()
+        assert out.dtype == torch.bfloat16
+        _close_bf16(out, expected)
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_fp8_caches_with_bf16_q_equal_the_bf16_kernel_bitwise(fmt, d):
+    # Unit scales: the same arithmetic as the bfloat16 kernel on PyTorch's
+    # widening of the codes to bf16, bit for bit, on random data and on every
+    # finite code.
+    import paged_attention_decode_amd as pad
+
+    q, k, v, bt, sl = _case([7, 300, 1500, 64], 16, 2, 4, d, seed=d + 3)
+    dt = FMTS[fmt]
+    codes = torch.arange(256, dtype=torch.uint8)
+    finite = codes[torch.isfinite(codes.view(dt).float())]
+    idx = torch.arange(k.numel())
+    every = finite[(idx * 7) % finite.numel()].view(k.shape).view(dt)
+    q = q * (1e-4 if fmt == "e5m2" else 1e-2)
+    qd, btd, sld = q.bfloat16().cuda(), bt.cuda(), sl.cuda()
+    for k8, v8 in ((k.to(dt), v.to(dt)), (every, v.to(dt))):
+        for splits in (None, 1, 8):
+            a = pad.paged_attention_decode_fp8(qd, k8.cuda(), v8.cuda(), btd, sld, num_splits=splits)
+            b = pad.paged_attention_decode_ex(qd, k8.bfloat16().cuda(), v8.bfloat16().cuda(), btd, sld,
+                                              num_splits=splits)
+            torch.cuda.synchronize()
+            assert torch.equal(a, b), (splits, (a.float() - b.float()).abs().max().item())
+
+
+def test_fp8_caches_with_bf16_q_through_csr_and_wrapper():
+    import paged_attention_decode_amd as pad
+
+    lens = [4096, 300, 2500, 1, 777, 0, 1500, 64]
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=45)
+    ks, vs = float(k.abs().max()) / 300.0, float(v.abs().max()) / 111.0
+    k8, v8 = _quant(k, "e4m3fn", ks), _quant(v, "e4m3fn", vs)
+    kd, vd, btd, sld = k8.cuda(), v8.cuda(), bt.cuda(), sl.cuda()
+    indptr, indices, last = _csr_of(bt, sl, 16)
+    qd = q.bfloat16().cuda()
+    w = pad.BatchDecodeWrapper()
+    w.plan(indptr, indices, last, 12, 2, 128, 16, q_data_type=torch.bfloat16, kv_data_type="e4m3fn")
+    a = w.run(qd, (kd, vd), k_scale=ks, v_scale=vs)
+    b = pad.paged_attention_decode_csr(qd, kd, vd, indptr, indices, last, k_scale=ks, v_scale=vs)
+    c = pad.paged_attention_decode_fp8(qd, kd, vd, btd, sld, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and a.dtype == torch.bfloat16
+    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs, q_dtype=torch.bfloat16)
+    _close_bf16(a, expected)
+    _close_bf16(c, expected)

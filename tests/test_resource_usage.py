@@ -25,12 +25,14 @@ def test_every_instantiation_is_reported(rows):
     # 5 head_dims x 6 block modes of the MFMA engine, plus the VALU engine's
     # (head_dim 64/128) x (uniform, other) x group sizes {1, 2, 4, 6, 8},
     # plus 2 fp8 cache formats x head_dim {64, 128, 256} x 6 block modes,
-    # plus bfloat16 x 5 head_dims x 6 block modes.
-    assert len(rows) >= 116
+    # plus bfloat16 x 5 head_dims x 6 block modes, plus the 2 fp8 formats
+    # with bfloat16 q x 3 head_dims x 6 block modes.
+    assert len(rows) >= 152
     assert any(r["template"] == "<128, 1, 0, 0>" for r in rows)  # the benchmark's kernel
     assert any(r["template"] == "<128, 1, 0, 0, e4m3fn>" for r in rows)
     assert any(r["template"] == "<128, 1, 0, 0, e5m2>" for r in rows)
     assert any(r["template"] == "<96, 0, 0, 0, bf16>" for r in rows)
+    assert any(r["template"] == "<256, 2, 0, 0, e5m2/bf16>" for r in rows)
 
 
 def test_no_scratch_memory_in_any_instantiation(rows):
