@@ -16,7 +16,8 @@ one set of inputs with ``--warm``.  Prints the per-call algorithmic bytes.
 (workloads.to_fp8) and calls ``paged_attention_decode_fp8``; the printed
 algorithmic bytes then count one byte per K/V element.  ``--kv bf16``
 rounds q and the caches to bfloat16 (workloads.to_bf16) and calls
-``paged_attention_decode_ex``.
+``paged_attention_decode_ex``.  With an fp8 ``--kv``, ``--q bf16`` rounds q
+to bfloat16 (fp8 caches with bf16 q and output).
 
 ``--planned`` plans every input set once with ``BatchDecodeWrapper``
 (the work-list planner kernel, one dispatch per set, before the timed
@@ -89,6 +90,7 @@ def main() -> None:
     p.add_argument("--repeats", type=int, default=8, help="--timeline: groups of 4 launches")
     p.add_argument("--json", default="", help="--timeline: write the table here")
     p.add_argument("--kv", default="fp16", choices=["fp16", "bf16", "e4m3fn", "e5m2"], help="q/K/V format")
+    p.add_argument("--q", default="fp16", choices=["fp16", "bf16"], help="q format with fp8 caches")
     p.add_argument("--planned", action="store_true",
                    help="plan every input set once (BatchDecodeWrapper), then time only run() calls")
     a = p.parse_args()
@@ -124,7 +126,10 @@ def main() -> None:
         def make(seed):
             if a.kv == "bf16":
                 return wl.to_bf16(make16(seed))
-            return wl.to_fp8(make16(seed), wl.FP8_NAMES[a.kv])
+            w8 = wl.to_fp8(make16(seed), wl.FP8_NAMES[a.kv])
+            if a.q == "bf16":
+                w8.q = w8.q.bfloat16()
+            return w8
     sets = _sets(make, a.warm)
     w0, n_sets = sets[0], len(sets)
     wraps = []
