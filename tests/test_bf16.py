@@ -149,3 +149,52 @@ def test_bf16_fuzz_matrix(seed):
     qd, kd, vd, btd, sld = _dev(q, k, v, bt, sl)
     for s in (None, 4, 60):
         _close(pad.paged_attention_decode_ex(qd, kd, vd, btd, sld, num_splits=s), expected)
+
+
+def test_bf16_strided_inputs():
+    import paged_attention_decode_amd as pad
+
+    lens = [40, 90]
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=41, spare=1, extra=0)
+    expected = decode_bf16_protocol(q, k, v, bt, sl)
+    n = k.shape[0]
+    qw = torch.zeros(2, 12, 256, dtype=torch.bfloat16, device="cuda")
+    qw[:, :, 64:192] = q.bfloat16().cuda()
+    kw = torch.zeros(n, 16, 3, 136, dtype=torch.bfloat16, device="cuda")
+    vw = torch.zeros(n, 16, 3, 136, dtype=torch.bfloat16, device="cuda")
+    kw[:, :, :2, :128] = k.bfloat16().cuda()
+    vw[:, :, :2, :128] = v.bfloat16().cuda()
+    out = pad.paged_attention_decode_ex(qw[:, :, 64:192], kw[:, :, :2, :128], vw[:, :, :2, :128], bt.cuda(),
+                                        sl.cuda())
+    torch.cuda.synchronize()
+    _close(out, expected)
+
+
+def test_bf16_graph_capture_replays():
+    import paged_attention_decode_amd as pad
+
+    lens = [4096, 300, 2500, 1]
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=93)
+    dev = [k.bfloat16().cuda(), v.bfloat16().cuda(), bt.cuda(), sl.cuda()]
+    qs = [torch.randn(len(lens), 12, 128, generator=torch.Generator().manual_seed(94 + i)).bfloat16().cuda()
+          for i in range(3)]
+    q_static = qs[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            pad.paged_attention_decode_ex(q_static, *dev)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out_static = pad.paged_attention_decode_ex(q_static, *dev)
+    torch.cuda.synchronize()
+    for rep in range(2):
+        for qn in qs:
+            q_static.copy_(qn)
+            graph.replay()
+            torch.cuda.synchronize()
+            eager = pad.paged_attention_decode_ex(qn, *dev)
+            torch.cuda.synchronize()
+            assert torch.equal(out_static, eager), f"replay {rep} differs from the eager call"

@@ -522,3 +522,32 @@ def test_fp8_caches_with_bf16_q_through_csr_and_wrapper():
     expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs, q_dtype=torch.bfloat16)
     _close_bf16(a, expected)
     _close_bf16(c, expected)
+
+
+@pytest.mark.parametrize("q_dtype", [torch.float16, torch.bfloat16])
+def test_fp8_strided_caches(q_dtype):
+    # fp8 caches as views of a wider buffer (an extra kv head, a padded row
+    # of 136 elements: strides in bytes, multiples of 8), q a slice of a
+    # wider tensor.
+    import paged_attention_decode_amd as pad
+
+    lens = [40, 90]
+    q, k, v, bt, sl = _case(lens, 16, 2, 6, 128, seed=61, spare=1, extra=0)
+    ks, vs = float(k.abs().max()) / 300.0, float(v.abs().max()) / 111.0
+    k8, v8 = _quant(k, "e4m3fn", ks), _quant(v, "e4m3fn", vs)
+    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs, q_dtype=q_dtype)
+    n = k.shape[0]
+    kw = torch.zeros(n, 16, 3, 136, dtype=torch.uint8, device="cuda")
+    vw = torch.zeros(n, 16, 3, 136, dtype=torch.uint8, device="cuda")
+    kw[:, :, :2, :128] = k8.view(torch.uint8).cuda()
+    vw[:, :, :2, :128] = v8.view(torch.uint8).cuda()
+    kv8 = kw.view(torch.float8_e4m3fn)[:, :, :2, :128]
+    vv8 = vw.view(torch.float8_e4m3fn)[:, :, :2, :128]
+    qw = torch.zeros(2, 12, 256, dtype=q_dtype, device="cuda")
+    qw[:, :, 64:192] = q.to(q_dtype).cuda()
+    out = pad.paged_attention_decode_fp8(qw[:, :, 64:192], kv8, vv8, bt.cuda(), sl.cuda(), k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    if q_dtype == torch.float16:
+        assert_parity(out.cpu(), expected)
+    else:
+        _close_bf16(out, expected)
