@@ -551,3 +551,27 @@ def test_fp8_strided_caches(q_dtype):
         assert_parity(out.cpu(), expected)
     else:
         _close_bf16(out, expected)
+
+
+@pytest.mark.parametrize("q_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("splits", [1, 5, 60])
+def test_fp8_wrapper_with_explicit_splits(q_dtype, splits):
+    # Work lists planned with an explicit split count (two-level merge at 60)
+    # equal the one-shot calls with the same count, dense and CSR.
+    import paged_attention_decode_amd as pad
+
+    lens = [4096, 300, 2500, 1, 777, 0]
+    q, k, v, bt, sl = _case(lens, 12, 2, 6, 128, seed=47)
+    ks, vs = float(k.abs().max()) / 300.0, float(v.abs().max()) / 111.0
+    k8, v8 = _quant(k, "e5m2", ks).cuda(), _quant(v, "e5m2", vs).cuda()
+    btd, sld, qd = bt.cuda(), sl.cuda(), q.to(q_dtype).cuda()
+    indptr, indices, last = _csr_of(bt, sl, 12)
+    wd, wc = pad.BatchDecodeWrapper(), pad.BatchDecodeWrapper()
+    wd.plan_block_table(btd, sld, 12, 2, 128, 12, num_splits=splits, kv_data_type="e5m2", q_data_type=q_dtype)
+    wc.plan(indptr, indices, last, 12, 2, 128, 12, num_splits=splits, kv_data_type="e5m2", q_data_type=q_dtype)
+    a = wd.run(qd, (k8, v8), k_scale=ks, v_scale=vs)
+    b = pad.paged_attention_decode_fp8(qd, k8, v8, btd, sld, k_scale=ks, v_scale=vs, num_splits=splits)
+    c = wc.run(qd, (k8, v8), k_scale=ks, v_scale=vs)
+    d = pad.paged_attention_decode_csr(qd, k8, v8, indptr, indices, last, num_splits=splits, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(c, d)
