@@ -10,7 +10,10 @@ TypeError).
 
 It is used as the parity oracle on fp16-rounded inputs (the protocol of
 tests/kernel_test_utils.py:47-51) and, timed on the host cores, as the CPU
-baseline.  It never ships in the product path.
+baseline.  It never ships in the product path.  decode_bf16_protocol and
+decode_fp8_protocol apply the same oracle to bfloat16-rounded and to
+dequantised fp8 inputs; tests/test_oracle_formats.py pins their own part
+(unit scales, the roles of k_scale, v_scale and q's rounding).
 """
 
 from __future__ import annotations
