@@ -415,8 +415,8 @@ FUZZ = int(__import__("os").environ.get("PAD_KERNEL_FUZZ_ITERS", "20"))
 
 @pytest.mark.parametrize("seed", range(FUZZ))
 def test_fp8_fuzz_matrix(seed):
-    # Both formats over head_dim 64/128/256, group sizes to 16, every block
-    # mode, ragged batches with empty rows, random non-power-of-two scales,
+    # Both formats, fp16 or bf16 q, over head_dim 64/128/256, group sizes to
+    # 16, every block mode, ragged batches with empty rows, random scales,
     # the heuristic plan, a fixed split and 60 splits (two-level merge),
     # dense and CSR; oracle parity on the dequantised caches.
     import random
@@ -426,22 +426,24 @@ def test_fp8_fuzz_matrix(seed):
 
     rng = random.Random(9000 + seed)
     fmt = rng.choice(list(FMTS))
+    q_dtype = rng.choice((torch.float16, torch.bfloat16))
     q, k, v, bt, sl = random_case(9100 + seed, kv_heads=(1, 2, 4), gqa=(1, 3, 8, 16), head_dims=(64, 128, 256),
                                   page_sizes=(1, 2, 3, 4, 8, 12, 16, 24, 32), min_len=0, max_len=400)
     ps = k.shape[1]
     ks = float(k.abs().max()) / rng.uniform(100.0, 400.0)
     vs = float(v.abs().max()) / rng.uniform(20.0, 400.0)
     k8, v8 = _quant(k, fmt, ks), _quant(v, fmt, vs)
-    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs)
-    qd, kd, vd = q.half().cuda(), k8.cuda(), v8.cuda()
+    expected = decode_fp8_protocol(q, k8, v8, bt, sl, ks, vs, q_dtype=q_dtype)
+    check = assert_parity if q_dtype == torch.float16 else _close_bf16
+    qd, kd, vd = q.to(q_dtype).cuda(), k8.cuda(), v8.cuda()
     indptr, indices, last = _csr_of(bt, sl, ps)
     for s in (None, 4, 60):
         a = pad.paged_attention_decode_fp8(qd, kd, vd, bt.cuda(), sl.cuda(), k_scale=ks, v_scale=vs, num_splits=s)
         b = pad.paged_attention_decode_csr(qd, kd, vd, indptr, indices, last, num_splits=s, k_scale=ks,
                                            v_scale=vs)
         torch.cuda.synchronize()
-        assert_parity(a.cpu(), expected)
-        assert_parity(b.cpu(), expected)
+        check(a.cpu(), expected)
+        check(b.cpu(), expected)
 
 
 # fp8 caches with bfloat16 q and output (PAD_KV_FP8_*_BF16): the codes widen
