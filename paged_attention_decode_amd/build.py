@@ -1,6 +1,7 @@
 """Build the native parts of the package in-tree.
 
-Four shared libraries, all written next to this file:
+Four shared libraries, all written next to this file (and one test program,
+below):
 
 * ``libpa_decode.so`` - the C-ABI library (``include/pa_decode.h``): gfx950
   kernels plus ``extern "C"`` entry points, compiled by ``hipcc`` from
@@ -15,6 +16,10 @@ Four shared libraries, all written next to this file:
   with ``-DPAD_TIMELINE``: every workgroup stamps the phases of its path
   (``include/pa_decode_timeline.h``) for ``profile_run --timeline``.
   Measurement only; the decode path never loads it.
+
+And one test program: ``tests/_bin/capi_consumer`` (``tests/capi_consumer.cpp``,
+host C++ linked to ``libpa_decode.so`` and the HIP runtime), a compiled
+caller of the C ABI that ``tests/test_capi_consumer.py`` runs.
 
 Usage: ``python -m paged_attention_decode_amd.build`` (or ``build()`` from
 ``__graft_entry__``).  Every call recompiles; the three hipcc builds run in
@@ -40,6 +45,7 @@ ARCH = "gfx950"
 CAPI_LIB = os.path.join(PKG_DIR, "libpa_decode.so")
 PROBE_LIB = os.path.join(PKG_DIR, "libpa_probe.so")
 TIMELINE_LIB = os.path.join(PKG_DIR, "libpa_decode_tl.so")
+CONSUMER_BIN = os.path.join(REPO_DIR, "tests", "_bin", "capi_consumer")
 EXT_NAME = "_pa_decode_ext"
 EXT_LIB = os.path.join(PKG_DIR, EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
 
@@ -138,12 +144,27 @@ def build_torch_ext() -> str:
     return EXT_LIB
 
 
+def build_capi_consumer() -> str:
+    """tests/_bin/capi_consumer: a compiled C ABI caller for tests/test_capi_consumer.py (host code only)."""
+    os.makedirs(os.path.dirname(CONSUMER_BIN), exist_ok=True)
+    tmp = CONSUMER_BIN + ".tmp"
+    _run([
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-D__HIP_PLATFORM_AMD__=1", f"-I{ROCM}/include",
+        f"-I{INCLUDE}", os.path.join(REPO_DIR, "tests", "capi_consumer.cpp"), "-o", tmp, f"-L{PKG_DIR}",
+        "-lpa_decode", f"-L{ROCM}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN/../../paged_attention_decode_amd",
+        f"-Wl,-rpath,{ROCM}/lib",
+    ])
+    os.replace(tmp, CONSUMER_BIN)
+    return CONSUMER_BIN
+
+
 def build_all() -> list[str]:
     with ThreadPoolExecutor(max_workers=3) as pool:
         hip = [pool.submit(build_capi), pool.submit(build_timeline), pool.submit(build_probe)]
         capi = hip[0].result()
         ext = build_torch_ext()  # links against libpa_decode.so
-        return [capi, ext, hip[1].result(), hip[2].result()]
+        consumer = build_capi_consumer()
+        return [capi, ext, consumer, hip[1].result(), hip[2].result()]
 
 
 if __name__ == "__main__":
