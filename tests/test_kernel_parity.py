@@ -107,6 +107,26 @@ def test_many_splits_few_rows(group, d):
         torch.testing.assert_close(out.float(), base, rtol=2e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("group,d", [(1, 64), (4, 64), (4, 128), (1, 128), (2, 256)])
+def test_folds_of_many_entries(group, d):
+    # The merging workgroup folds a unit's entries in one batch of 4, 8 or
+    # 16, or in batches of 16 in turn beyond 16 (here 17 to 47 splits, the
+    # last batch ragged), and the group results of two-level merges (stride
+    # 16; 300 splits give 19 groups, two batches), with plans of 1 to 8
+    # waves per workgroup and 16 to 128 (row, 4 columns) elements per unit.
+    # Against the oracle and against one split.
+    lens = [16 * 600, 16 * 13 + 5, 16 * 29, 16 * 5 + 1, 16 * 48]
+    hkv = 2
+    bt, total = contiguous_table(lens, 16)
+    k, v = make_cache(total + 1, 16, hkv, d, seed=1200 + d + group)
+    q = torch.randn(len(lens), hkv * group, d, generator=torch.Generator().manual_seed(1201 + d + group))
+    sl = torch.tensor(lens, dtype=torch.int32)
+    base = _run(q, k, v, bt, sl, 0, num_splits=1).float()
+    for s in (5, 17, 20, 33, 48, 75, 300, 600):
+        out = _check(q, k, v, bt, sl, 0, s)
+        torch.testing.assert_close(out.float(), base, rtol=2e-3, atol=1e-3)
+
+
 @pytest.mark.parametrize("num_splits", [60, 100, 200])
 def test_two_level_merge(num_splits):
     # More than 48 splits of one sequence merge in two levels: groups of 16
