@@ -1769,8 +1769,10 @@ static size_t workspace_layout(const pad_decode_dims* d, int S, void* ws, float*
   return 256 + o_bytes + rows * sizeof(float2);
 }
 
-// Splits per unit on an oversubscribed grid (see oversubscribed_shape).
+// Splits per unit on an oversubscribed grid (see oversubscribed_shape), at
+// least; and at least this many workgroups per CU.
 constexpr int kOversubscribeSplits = 4;
+constexpr int kOversubscribeGroupsPerCu = 8;
 
 // A bandwidth-bound shape with at least one (sequence, kv head) unit per CU
 // and a batch the in-kernel planner handles.  One workgroup per unit would
@@ -1785,6 +1787,19 @@ static bool oversubscribed_shape(const pad_decode_dims* d, int num_splits, int n
   const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
   return num_splits == 0 && !latency_bound && units >= num_cus && d->batch <= kPlanMaxBatch &&
          d->max_pages < (1 << 23);
+}
+
+// Items per unit of an oversubscribed grid: kOversubscribeSplits, or more
+// below two units per CU, so that the grid holds kOversubscribeGroupsPerCu
+// workgroups per CU and a ragged batch's long units end in several smaller
+// items.  Measured on C5's lengths (batch 256, page 16, 512-32768 tokens)
+// with 4 / 8 / 16 items per unit: 256 units (one GPU's share of C5 over 8
+// GPUs by kv heads, 8/1 heads) 426 / 391 / 403 us; 512 units 759 / 750 /
+// 803 us; 1024 units 1463 / 1509 / 1606 us; the whole C5, 2048 units,
+// 2833 / 2916 / 3164 us.
+static int64_t oversubscribe_splits(int64_t units, int num_cus) {
+  const int64_t want = ((int64_t)kOversubscribeGroupsPerCu * num_cus + units - 1) / units;
+  return want > kOversubscribeSplits ? want : kOversubscribeSplits;
 }
 
 // Pages of one sequence the plan assumes: the dense table's row width, or
@@ -1839,7 +1854,7 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     const int64_t max_groups = latency_bound ? num_cus / 2 : num_cus;
     int64_t s_want = 1;
     while (s_want * 2 * units <= max_groups) s_want *= 2;
-    if (oversubscribed_shape(d, num_splits, num_cus, latency_bound)) s_want = kOversubscribeSplits;
+    if (oversubscribed_shape(d, num_splits, num_cus, latency_bound)) s_want = oversubscribe_splits(units, num_cus);
     int64_t s_cap = blocks_per_seq / kMinBlocks;
     // Latency-bound short sequences: a wave's serial chain of blocks costs
     // more than a merge of up to 16 splits (one round trip), so splits may

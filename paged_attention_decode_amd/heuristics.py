@@ -15,9 +15,10 @@ least 16 blocks of 16 tokens per split; bandwidth-bound shapes get one
 4-wave workgroup per CU, latency-bound ones (at most 16 blocks of work per
 CU) 8-wave workgroups on at most half the CUs.  Bandwidth-bound shapes with
 at least one (sequence, kv head) unit per CU and batch <= 256 get a grid of
-OVERSUBSCRIBE_SPLITS items per unit, which the kernel fills from the
-lengths: one item per unit when every sequence is full, equal page chunks
-otherwise.
+OVERSUBSCRIBE_SPLITS items per unit (more below two units per CU, so that
+the grid holds OVERSUBSCRIBE_GROUPS_PER_CU workgroups per CU), which the
+kernel fills from the lengths: one item per unit when every sequence is
+full, equal page chunks otherwise.
 """
 
 from __future__ import annotations
@@ -30,7 +31,8 @@ MAX_SPLITS = 1024          # PAD_MAX_SPLITS
 MIN_BLOCKS = 16            # 16-token blocks per split, at least
 MIN_BLOCKS_SHORT = 4       # the same for short latency-bound sequences (<= 16 splits)
 LDS_BUDGET = 136 * 1024    # LDS of one workgroup: wave merge + MFMA staging
-OVERSUBSCRIBE_SPLITS = 4   # items per unit on an oversubscribed grid
+OVERSUBSCRIBE_SPLITS = 4   # items per unit on an oversubscribed grid, at least,
+OVERSUBSCRIBE_GROUPS_PER_CU = 8  # and at least this many workgroups per CU
 PLAN_MAX_BATCH = 256       # largest batch the in-kernel planner handles
 TWO_LEVEL_SPLITS = 48      # units with more splits merge in two levels (groups of 16)
 
@@ -89,7 +91,7 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
         while want * 2 * units <= max_groups:
             want *= 2
         if oversubscribed(batch, num_kv_heads, max_pages, latency_bound, num_cus):
-            want = OVERSUBSCRIBE_SPLITS
+            want = max(OVERSUBSCRIBE_SPLITS, _cdiv(OVERSUBSCRIBE_GROUPS_PER_CU * num_cus, units))
         cap = blocks_per_seq // MIN_BLOCKS
         if latency_bound:  # short sequences: down to 4 blocks per split, at most 16 splits
             cap = max(cap, min(blocks_per_seq // MIN_BLOCKS_SHORT, 16))

@@ -4,6 +4,9 @@
 
 ``--shape B/HQ/HKV/D/L[/PS]`` replaces the configuration by B sequences of L
 tokens (page size PS, default 16) with HQ / HKV heads of head_dim D.
+``--tp N`` / ``--sp N`` run one GPU's share of the configuration when it is
+sharded over N GPUs by kv heads or by ranges of each sequence's pages
+(workloads.make).
 
 Runs a calibration copy first (``--copy-mb`` MiB read and written by
 PyTorch's copy kernel, 3 dispatches: the bytes a FETCH_SIZE / WRITE_SIZE
@@ -85,6 +88,8 @@ def main() -> None:
     p.add_argument("--copy-mb", type=int, default=256)
     p.add_argument("--warm", action="store_true")
     p.add_argument("--shape", default="", help="B/HQ/HKV/D/L[/PS]: uniform lengths instead of --config")
+    p.add_argument("--tp", type=int, default=1, help="--config: one GPU's share over N GPUs by kv heads")
+    p.add_argument("--sp", type=int, default=1, help="--config: one GPU's share over N GPUs by page ranges")
     p.add_argument("--timeline", action="store_true", help="per-phase budget from libpa_decode_tl.so")
     p.add_argument("--configs", default="C2:16,C2:32,C2:64,C3,C4", help="--timeline: configurations")
     p.add_argument("--repeats", type=int, default=8, help="--timeline: groups of 4 launches")
@@ -118,7 +123,7 @@ def main() -> None:
             return wl._build(f"shape {a.shape}", [seq] * b, hq, hkv, d, ps, seed, "cuda")
     else:
         def make(seed):
-            return wl.make(a.config, batch=a.batch, seed=seed)
+            return wl.make(a.config, batch=a.batch, seed=seed, tp=a.tp, sp=a.sp)
     if a.kv != "fp16":
         assert not a.planned, "--planned runs fp16 caches"
         make16 = make

@@ -18,6 +18,10 @@ and within sequences; unused block_table columns point at valid pages):
 valid token, the q read and the output write, the block_table entries of the
 used pages and seq_lens (the split workspace is excluded as overhead).
 
+``make(..., tp=N)`` and ``make(..., sp=N)`` build one GPU's share of a
+configuration sharded over N GPUs, by kv heads or by ranges of each
+sequence's pages.
+
 ``to_bf16`` rounds q and the caches to bfloat16.  ``to_fp8`` turns a
 workload's caches into fp8 codes (float8_e4m3fn or
 float8_e5m2) of K / k_scale and V / v_scale, per-tensor scales chosen so the
@@ -115,21 +119,50 @@ def c3_seq_lens(seed: int, batch: int = 32, max_len: int = 8192, page_size: int 
     return lens
 
 
-def make(name: str, batch: int | None = None, seed: int = 0, device: str = "cuda") -> Workload:
+def _spec(name: str, batch: int | None, seed: int):
+    """(label, seq_lens, hq, hkv, head_dim, page_size, extra _build arguments) of a configuration."""
     if name == "C1":
-        return _build("C1", [1024], 12, 2, 128, 16, seed, device)
+        return "C1", [1024], 12, 2, 128, 16, {}
     if name == "C2":
         b = 64 if batch is None else batch
-        return _build(f"C2_b{b}", [4096] * b, 12, 2, 128, 16, seed, device)
+        return f"C2_b{b}", [4096] * b, 12, 2, 128, 16, {}
     if name == "C3":
-        return _build("C3", c3_seq_lens(seed), 12, 2, 128, 32, seed, device, max_pages=256, key_boost=2)
+        return "C3", c3_seq_lens(seed), 12, 2, 128, 32, {"max_pages": 256, "key_boost": 2}
     if name == "C4":
-        return _build("C4", [131072], 32, 8, 128, 16, seed, device)
+        return "C4", [131072], 32, 8, 128, 16, {}
     if name == "C5":
         g = torch.Generator().manual_seed(seed)
         lens = torch.randint(512, 32768 + 1, (256,), generator=g).tolist()
-        return _build("C5", lens, 64, 8, 128, 16, seed, device, max_pages=2048)
+        return "C5", lens, 64, 8, 128, 16, {"max_pages": 2048}
     raise ValueError(f"unknown workload {name}")
+
+
+def shard_lens(lens, page_size: int, sp: int) -> list[int]:
+    """Tokens of each sequence on the first of ``sp`` GPUs that hold consecutive ranges of its
+    pages, ceil(pages / sp) pages each (the last GPU holding the remainder): one GPU's share."""
+    out = []
+    for n in lens:
+        pages = -(-n // page_size)
+        out.append(min(n, -(-pages // sp) * page_size))
+    return out
+
+
+def make(name: str, batch: int | None = None, seed: int = 0, device: str = "cuda", tp: int = 1,
+         sp: int = 1) -> Workload:
+    """Configuration ``name``, or one GPU's share of it when it is sharded: ``tp`` GPUs each holding
+    num_kv_heads / tp kv heads and their query groups (tensor parallel over heads), or ``sp`` GPUs
+    each holding a range of every sequence's pages (``shard_lens``; the split-K merge of the
+    shares would follow on each GPU)."""
+    label, lens, hq, hkv, d, ps, kw = _spec(name, batch, seed)
+    if tp < 1 or sp < 1 or hkv % tp:
+        raise ValueError(f"{name}: tp {tp} must divide {hkv} kv heads, sp {sp} must be >= 1")
+    if tp > 1:
+        label, hq, hkv = f"{label}_tp{tp}", hq // tp, hkv // tp
+    if sp > 1:
+        label, lens = f"{label}_sp{sp}", shard_lens(lens, ps, sp)
+        if "max_pages" in kw:
+            kw = dict(kw, max_pages=-(-kw["max_pages"] // sp))
+    return _build(label, lens, hq, hkv, d, ps, seed, device, **kw)
 
 
 def bytes_of(w: Workload) -> int:

@@ -92,3 +92,37 @@ def test_fp8_workload_conversion():
         assert torch.all((deq - w.k_cache.float()).abs()[big] <= rel / 2 * w.k_cache.float().abs()[big] + 1e-6)
         kv16 = 2 * 4096 * 2 * 128 * 2 * 2  # batch x seq x kv heads x head_dim x fp16 x (K, V)
         assert wl.bytes_of(w) - wl.bytes_of(w8) == kv16 // 2
+
+
+def test_shard_shares_of_a_configuration():
+    # One GPU's share of a sharded configuration (workloads.make tp= / sp=).
+    # Page ranges: counting every token of a sequence onto GPU (t // ps) // c,
+    # with c = ceil(pages / sp) pages per GPU, gives GPU 0's share, and the
+    # shares of all GPUs add up to the sequence.
+    g = torch.Generator().manual_seed(0)
+    for _ in range(200):
+        n = int(torch.randint(1, 5000, (1,), generator=g))
+        ps = int(torch.randint(1, 40, (1,), generator=g))
+        sp = int(torch.randint(1, 10, (1,), generator=g))
+        c = -(-(-(-n // ps)) // sp)
+        owner = [(t // ps) // c for t in range(n)]
+        assert wl.shard_lens([n], ps, sp) == [owner.count(0)]
+        assert sum(owner.count(i) for i in range(sp)) == n and max(owner) < sp
+    # kv heads: 1/tp of the heads with the same lengths, 1/tp of the K/V bytes.
+    full, share = wl.make("C2", batch=4, seed=5, device="cpu"), wl.make("C2", batch=4, seed=5, device="cpu", tp=2)
+    assert share.q.shape == (4, 6, 128) and share.k_cache.shape[2] == 1 and share.name == "C2_b4_tp2"
+    assert torch.equal(share.seq_lens, full.seq_lens)
+    kv = lambda w: w.k_cache[0, 0].numel() * 2 * 2 * int(w.seq_lens.sum())  # noqa: E731  (K, V) fp16
+    assert kv(full) == 2 * kv(share)
+    c4 = wl.make("C4", device="cpu", sp=8)
+    assert c4.seq_lens.tolist() == [16384] and c4.block_table.shape == (1, 1024) and c4.q.shape == (1, 32, 128)
+    c3 = wl.make("C3", seed=2, device="cpu", sp=2)
+    assert c3.block_table.shape[1] == 128 and all(0 < n <= 4096 for n in c3.seq_lens.tolist())
+    # no sharding: the configuration itself
+    assert torch.equal(wl.make("C1", seed=4, device="cpu", tp=1, sp=1).k_cache, wl.make("C1", seed=4, device="cpu").k_cache)
+    for bad in ({"tp": 3}, {"tp": 0}, {"sp": 0}):
+        try:
+            wl.make("C2", batch=1, device="cpu", **bad)
+        except ValueError:
+            continue
+        raise AssertionError(bad)

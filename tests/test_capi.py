@@ -238,13 +238,18 @@ def test_heuristic_properties():
     p64 = heuristics.plan(64, 12, 2, 128, 16, 256)
     assert p64.num_splits <= 8
     # At least one unit per CU: a grid of 4 items per unit for the in-kernel
-    # planner (one item per unit if every sequence is full); past the
-    # planner's batch limit, one workgroup per unit.
+    # planner (one item per unit if every sequence is full), and at least 8
+    # workgroups per CU (8 items per unit at one unit per CU, 5 at 410
+    # units); past the planner's batch limit, one workgroup per unit.
     p_big = heuristics.plan(256, 64, 8, 128, 16, 2048)
-    assert p_big.num_splits == heuristics.OVERSUBSCRIBE_SPLITS and not p_big.single_pass
-    assert p_big.workspace_bytes == heuristics.workspace_bytes(256, 8, 8, 128, heuristics.OVERSUBSCRIBE_SPLITS)
+    assert p_big.num_splits == heuristics.OVERSUBSCRIBE_SPLITS == 4 and not p_big.single_pass
+    assert p_big.workspace_bytes == heuristics.workspace_bytes(256, 8, 8, 128, 4)
     p128 = heuristics.plan(128, 12, 2, 128, 16, 256)
-    assert p128.num_splits == heuristics.OVERSUBSCRIBE_SPLITS and p128.waves_per_group == 4
+    assert p128.num_splits == 8 and p128.waves_per_group == 4
+    p_share = heuristics.plan(256, 8, 1, 128, 16, 2048)  # C5 over 8 GPUs by kv heads: 256 units
+    assert p_share.num_splits == 8 and p_share.workspace_bytes == heuristics.workspace_bytes(256, 1, 8, 128, 8)
+    assert heuristics.plan(205, 12, 2, 128, 16, 256).num_splits == 5  # 410 units: 2050 workgroups
+    assert heuristics.plan(256, 8, 2, 128, 16, 2048).num_splits == 4  # 512 units
     p_over = heuristics.plan(512, 12, 2, 128, 16, 256)
     assert p_over.num_splits == 1 and p_over.single_pass
 
