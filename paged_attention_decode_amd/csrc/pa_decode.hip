@@ -1774,29 +1774,35 @@ static size_t workspace_layout(const pad_decode_dims* d, int S, void* ws, float*
 constexpr int kOversubscribeSplits = 4;
 constexpr int kOversubscribeGroupsPerCu = 8;
 
-// A bandwidth-bound shape with at least one (sequence, kv head) unit per CU
-// and a batch the in-kernel planner handles.  One workgroup per unit would
-// be enough for uniform lengths (measured: C2 batch 128 81.4 us with one
-// split against 93.9 us with 4), but ragged ones leave their longest units
-// running alone at the end (C5: 2930 us with one workgroup per unit,
-// 2656 us with kOversubscribeSplits planned items per unit, 2767 us with 8).
-// The launch therefore sizes the grid for kOversubscribeSplits items per
-// unit and the kernel decides from the lengths: all at full capacity, one
-// item per unit; otherwise equal page chunks.
+// A bandwidth-bound shape with more than one (sequence, kv head) unit per
+// two CUs, where the power-of-two rule gives one split per unit, and a batch
+// the in-kernel planner handles.  One workgroup per unit would be enough for
+// uniform lengths (measured: C2 batch 128 81.4 us with one split against
+// 93.9 us with 4 static splits), but ragged ones leave their longest units
+// running alone at the end (C5: 2930 us with one workgroup per unit, 2656 us
+// with kOversubscribeSplits planned items per unit, 2767 us with 8; C3's
+// lengths at batch 66-127, 132-254 units: 101-113 us with one workgroup per
+// unit, 58-100 us planned over oversubscribe_splits items per unit).  The
+// launch therefore sizes the grid for several items per unit and the kernel
+// decides from the lengths: all at full capacity, one item per unit;
+// otherwise equal page chunks.
 static bool oversubscribed_shape(const pad_decode_dims* d, int num_splits, int num_cus, bool latency_bound) {
   const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
-  return num_splits == 0 && !latency_bound && units >= num_cus && d->batch <= kPlanMaxBatch &&
+  return num_splits == 0 && !latency_bound && units * 2 > num_cus && d->batch <= kPlanMaxBatch &&
          d->max_pages < (1 << 23);
 }
 
 // Items per unit of an oversubscribed grid: kOversubscribeSplits, or more
 // below two units per CU, so that the grid holds kOversubscribeGroupsPerCu
 // workgroups per CU and a ragged batch's long units end in several smaller
-// items.  Measured on C5's lengths (batch 256, page 16, 512-32768 tokens)
-// with 4 / 8 / 16 items per unit: 256 units (one GPU's share of C5 over 8
-// GPUs by kv heads, 8/1 heads) 426 / 391 / 403 us; 512 units 759 / 750 /
-// 803 us; 1024 units 1463 / 1509 / 1606 us; the whole C5, 2048 units,
-// 2833 / 2916 / 3164 us.
+// items (up to 16 items just above one unit per two CUs).  Measured on C5's
+// lengths (batch 256, page 16, 512-32768 tokens) with 4 / 8 / 16 items per
+// unit: 256 units (one GPU's share of C5 over 8 GPUs by kv heads, 8/1
+// heads) 426 / 391 / 403 us; 512 units 759 / 750 / 803 us; 1024 units
+// 1463 / 1509 / 1606 us; the whole C5, 2048 units, 2833 / 2916 / 3164 us.
+// On C3's lengths (1-8192 tokens, page 32) this rule and a flat 4 items
+// tie: 132 / 160 / 192 / 254 units 59.6 / 70.4 / 79.3 / 99.7 us against
+// 58.1 / 72.0 / 76.3 / 104.9 us.
 static int64_t oversubscribe_splits(int64_t units, int num_cus) {
   const int64_t want = ((int64_t)kOversubscribeGroupsPerCu * num_cus + units - 1) / units;
   return want > kOversubscribeSplits ? want : kOversubscribeSplits;

@@ -14,7 +14,7 @@ C2 (batch 1-64), C3 and C4 on MI355X: a power-of-two split count with at
 least 16 blocks of 16 tokens per split; bandwidth-bound shapes get one
 4-wave workgroup per CU, latency-bound ones (at most 16 blocks of work per
 CU) 8-wave workgroups on at most half the CUs.  Bandwidth-bound shapes with
-at least one (sequence, kv head) unit per CU and batch <= 256 get a grid of
+more than one (sequence, kv head) unit per two CUs and batch <= 256 get a grid of
 OVERSUBSCRIBE_SPLITS items per unit (more below two units per CU, so that
 the grid holds OVERSUBSCRIBE_GROUPS_PER_CU workgroups per CU), which the
 kernel fills from the lengths: one item per unit when every sequence is
@@ -118,8 +118,8 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
 
 
 def oversubscribed(batch: int, num_kv_heads: int, max_pages: int, latency_bound: bool, num_cus: int) -> bool:
-    """Heuristic shape with a unit per CU or more, planned in-kernel over an oversubscribed grid."""
-    return (not latency_bound and max(batch, 1) * num_kv_heads >= num_cus and batch <= PLAN_MAX_BATCH
+    """Heuristic shape with more than one unit per two CUs, planned in-kernel over an oversubscribed grid."""
+    return (not latency_bound and max(batch, 1) * num_kv_heads * 2 > num_cus and batch <= PLAN_MAX_BATCH
             and max_pages < (1 << 23))
 
 

@@ -237,10 +237,10 @@ def test_heuristic_properties():
         assert p.waves_per_group == 4 and p.num_splits * b * 2 == 256
     p64 = heuristics.plan(64, 12, 2, 128, 16, 256)
     assert p64.num_splits <= 8
-    # At least one unit per CU: a grid of 4 items per unit for the in-kernel
-    # planner (one item per unit if every sequence is full), and at least 8
-    # workgroups per CU (8 items per unit at one unit per CU, 5 at 410
-    # units); past the planner's batch limit, one workgroup per unit.
+    # More than one unit per two CUs: a grid of 4 items per unit for the
+    # in-kernel planner (one item per unit if every sequence is full), and at
+    # least 8 workgroups per CU (8 items per unit at one unit per CU, 5 at
+    # 410 units); past the planner's batch limit, one workgroup per unit.
     p_big = heuristics.plan(256, 64, 8, 128, 16, 2048)
     assert p_big.num_splits == heuristics.OVERSUBSCRIBE_SPLITS == 4 and not p_big.single_pass
     assert p_big.workspace_bytes == heuristics.workspace_bytes(256, 8, 8, 128, 4)
@@ -250,6 +250,11 @@ def test_heuristic_properties():
     assert p_share.num_splits == 8 and p_share.workspace_bytes == heuristics.workspace_bytes(256, 1, 8, 128, 8)
     assert heuristics.plan(205, 12, 2, 128, 16, 256).num_splits == 5  # 410 units: 2050 workgroups
     assert heuristics.plan(256, 8, 2, 128, 16, 2048).num_splits == 4  # 512 units
+    # From more than one unit per two CUs (where one split per unit would leave a ragged batch's
+    # long units to one workgroup each); at most one unit per two CUs keeps the power-of-two rule.
+    assert heuristics.plan(96, 12, 2, 128, 16, 256).num_splits == 11  # 192 units: 2112 workgroups
+    assert heuristics.plan(65, 12, 2, 128, 16, 256).num_splits == 16  # 130 units
+    assert heuristics.plan(64, 12, 2, 128, 16, 256).num_splits == 2  # 128 units: C2 batch 64
     p_over = heuristics.plan(512, 12, 2, 128, 16, 256)
     assert p_over.num_splits == 1 and p_over.single_pass
 
