@@ -114,8 +114,9 @@ struct Phase1Args {
   int ps_shift;    // log2(ps) when ps is a power of two, else -1
   int csr;         // 1: page ids from (indptr, indices, last_page_len)
   int balance;     // 1: items planned from the sequence lengths in-kernel;
-                   // 2: the same on an oversubscribed grid (one item per
-                   //    unit when every sequence is full)
+                   // 2: the same on an oversubscribed grid (the static
+                   //    splits, pps pages each, on the first workgroups
+                   //    when every sequence is full)
   int min_chunk;   // planner: fewest pages per item
   int pair_heads;  // 1: workgroups 8 apart take kv heads 2m and 2m+1 (see grid_pos)
   int wl_key;      // key of the launch's plan, matched against the work list's header
@@ -1275,9 +1276,9 @@ __device__ __forceinline__ WorkItem static_item(const Phase1Args& a, int s, int 
 
 // Planned mode: read every sequence length; with every sequence at full
 // capacity the static split is already even (balance == 1) or, on an
-// oversubscribed grid (balance == 2: at least as many (sequence, kv head)
-// units as CUs), each unit is one item of workgroup g = unit and the other
-// workgroups exit; otherwise plan the items.
+// oversubscribed grid (balance == 2), the static splits run on the first
+// workgroups (one item per unit, workgroup g = unit, when the static rule
+// gives one split) and the other workgroups exit; otherwise plan the items.
 template <int NK>
 __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, const SeqRaw& raw, int s, int h, int bz, int g,
                                                  int G, int lin, const int32_t* static_row, int lane) {
@@ -1287,6 +1288,30 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, const SeqR
   for (int k = 0; k < NK; ++k)
     if (lane + 64 * k < a.batch && t.pages[k] != a.max_pages) full = false;
   if (__builtin_amdgcn_ballot_w64(!full) == 0) {
+    const int s0 = a.balance == 2 && a.pps > 0 && a.max_pages > a.pps ? (a.max_pages + a.pps - 1) / a.pps : 1;
+    if (s0 > 1) {
+      // The static splits, s0 per unit (pps pages each), on the first
+      // units * s0 workgroups in order: unit g / s0, split g % s0, whose
+      // partials take the unit's s0 consecutive slots.  The launch keeps
+      // head pairing off here, so g is the linear workgroup index and the
+      // active workgroups spread over the XCDs.
+      WorkItem w;
+      const int units = a.batch * a.hkv;
+      const int q = g / s0;
+      const int u = min(q, units - 1);
+      w.b = u / a.hkv;
+      w.kvh = u - w.b * a.hkv;
+      w.p_begin = (g - q * s0) * a.pps;
+      w.p_end = min(w.p_begin + a.pps, a.max_pages);
+      w.L = seq_lane_value<NK>(t.len, w.b);
+      w.nsplit = s0;
+      w.slot0 = q * s0;
+      w.col_max = a.max_pages - 1;
+      w.valid = q < units;
+      w.ids_row = a.bt + (int64_t)w.b * a.sbb;
+      w.ids_stride = a.sbp;
+      return w;
+    }
     if (a.balance == 2) {
       WorkItem w;
       const int units = a.batch * a.hkv;
@@ -1774,22 +1799,24 @@ static size_t workspace_layout(const pad_decode_dims* d, int S, void* ws, float*
 constexpr int kOversubscribeSplits = 4;
 constexpr int kOversubscribeGroupsPerCu = 8;
 
-// A bandwidth-bound shape with more than one (sequence, kv head) unit per
-// two CUs, where the power-of-two rule gives one split per unit, and a batch
-// the in-kernel planner handles.  One workgroup per unit would be enough for
-// uniform lengths (measured: C2 batch 128 81.4 us with one split against
-// 93.9 us with 4 static splits), but ragged ones leave their longest units
-// running alone at the end (C5: 2930 us with one workgroup per unit, 2656 us
-// with kOversubscribeSplits planned items per unit, 2767 us with 8; C3's
-// lengths at batch 66-127, 132-254 units: 101-113 us with one workgroup per
-// unit, 58-100 us planned over oversubscribe_splits items per unit).  The
-// launch therefore sizes the grid for several items per unit and the kernel
-// decides from the lengths: all at full capacity, one item per unit;
-// otherwise equal page chunks.
+// A bandwidth-bound shape with a batch the in-kernel planner handles and
+// either more than one (sequence, kv head) unit per two CUs, where the
+// power-of-two rule gives one split per unit, or more than one per four CUs
+// where its two splits per unit leave CUs idle.  The static splits are
+// enough for uniform lengths (measured: C2 batch 128 81.4 us with one split
+// against 93.9 us with 4 static splits), but ragged ones leave their longest
+// units running alone at the end (C5: 2930 us with one workgroup per unit,
+// 2656 us with kOversubscribeSplits planned items per unit, 2767 us with 8;
+// C3's lengths at batch 66-127, 132-254 units: 101-113 us with one
+// workgroup per unit, 58-100 us planned over oversubscribe_splits items per
+// unit; at batch 33-48, 66-96 units: 51-53 us with two splits per unit,
+// 34-46 us planned).  The launch therefore sizes the grid for several items
+// per unit and the kernel decides from the lengths: all at full capacity,
+// the static splits on the first workgroups; otherwise equal page chunks.
 static bool oversubscribed_shape(const pad_decode_dims* d, int num_splits, int num_cus, bool latency_bound) {
   const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
-  return num_splits == 0 && !latency_bound && units * 2 > num_cus && d->batch <= kPlanMaxBatch &&
-         d->max_pages < (1 << 23);
+  const bool many = units * 2 > num_cus || (units * 4 > num_cus && units * 2 < num_cus);
+  return num_splits == 0 && !latency_bound && many && d->batch <= kPlanMaxBatch && d->max_pages < (1 << 23);
 }
 
 // Items per unit of an oversubscribed grid: kOversubscribeSplits, or more
@@ -1826,8 +1853,11 @@ static bool latency_bound_shape(const pad_decode_dims* d, int num_cus, bool csr)
 }
 
 // kv_bytes: bytes per K/V element (2 for fp16, 1 for fp8 caches).
+// pps_full, if given, receives the pages per split of the static splits
+// (the power-of-two rule), which an oversubscribed grid runs when every
+// sequence is at full capacity.
 static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int engine, bool csr,
-                     pad_decode_plan_t* p, int kv_bytes = 2) {
+                     pad_decode_plan_t* p, int kv_bytes = 2, int* pps_full = nullptr) {
   const int st = validate_dims(d);
   if (st != PAD_OK) return st;
   if (num_splits < 0 || num_splits > PAD_MAX_SPLITS) return PAD_ERR_NUM_SPLITS;
@@ -1852,6 +1882,7 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     // Splits past a sequence's last page are empty (never read).
     S = num_splits;
     pps = ceil_div(max_pages, S);
+    if (pps_full) *pps_full = pps;
   } else {
     // A power-of-two split count (the splits of a power-of-two page count
     // are then equal) with at least kMinBlocks 16-token blocks per split, so
@@ -1860,6 +1891,7 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     const int64_t max_groups = latency_bound ? num_cus / 2 : num_cus;
     int64_t s_want = 1;
     while (s_want * 2 * units <= max_groups) s_want *= 2;
+    int64_t s_static = s_want;
     if (oversubscribed_shape(d, num_splits, num_cus, latency_bound)) s_want = oversubscribe_splits(units, num_cus);
     int64_t s_cap = blocks_per_seq / kMinBlocks;
     // Latency-bound short sequences: a wave's serial chain of blocks costs
@@ -1873,6 +1905,8 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     if (s_cap < 1) s_cap = 1;
     if (s_want > s_cap) s_want = s_cap;
     if (s_want > PAD_MAX_SPLITS) s_want = PAD_MAX_SPLITS;
+    if (s_static > s_want) s_static = s_want;
+    if (pps_full) *pps_full = ceil_div(max_pages, s_static);
     if (csr) {
       // Never more splits (hence scratch) than the dense plan of the same
       // dims, so pad_decode_workspace_bytes() also sizes a CSR launch.
@@ -2045,7 +2079,8 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   if (st != PAD_OK) return st;
   const bool csr = indptr != nullptr || lpl != nullptr;
   pad_decode_plan_t& plan = L->plan;
-  st = plan_impl(d, num_splits, cus, engine, csr, &plan, kv_bytes);
+  int pps_full = 0;
+  st = plan_impl(d, num_splits, cus, engine, csr, &plan, kv_bytes, &pps_full);
   if (st != PAD_OK) return st;
   const int gqa = d->num_q_heads / d->num_kv_heads;
   if (engine == 1 && !valu_supported(d->head_dim, gqa)) return PAD_ERR_UNSUPPORTED_GQA;
@@ -2114,6 +2149,14 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   a.min_chunk = ceil_div(kMinBlocks * kBlockTokens, d->page_size);
   a.pair_heads = ((d->head_dim * 2) % 128 != 0 && d->num_kv_heads % 2 == 0 &&
                   ((int64_t)S * d->num_kv_heads * d->batch) % 16 == 0) ? 1 : 0;
+  if (a.balance == 2) {
+    // An oversubscribed grid runs the static splits when every sequence is
+    // at full capacity: pps is theirs (the grid's own split is the planner's
+    // business).  With more than one static split per unit they take the
+    // first workgroups in order, unit-major, so head pairing stays off.
+    a.pps = pps_full;
+    if (ceil_div(d->max_pages, pps_full) > 1) a.pair_heads = 0;
+  }
   a.ps_shift = -1;
   for (int sh = 0; sh < 31; ++sh)
     if ((1 << sh) == d->page_size) a.ps_shift = sh;

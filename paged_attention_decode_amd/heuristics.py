@@ -17,8 +17,10 @@ CU) 8-wave workgroups on at most half the CUs.  Bandwidth-bound shapes with
 more than one (sequence, kv head) unit per two CUs and batch <= 256 get a grid of
 OVERSUBSCRIBE_SPLITS items per unit (more below two units per CU, so that
 the grid holds OVERSUBSCRIBE_GROUPS_PER_CU workgroups per CU), which the
-kernel fills from the lengths: one item per unit when every sequence is
-full, equal page chunks otherwise.
+kernel fills from the lengths: the static splits of the power-of-two rule
+when every sequence is full, equal page chunks otherwise.  The same holds
+from more than one unit per four CUs, where two static splits per unit
+would leave CUs idle.
 """
 
 from __future__ import annotations
@@ -118,9 +120,11 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
 
 
 def oversubscribed(batch: int, num_kv_heads: int, max_pages: int, latency_bound: bool, num_cus: int) -> bool:
-    """Heuristic shape with more than one unit per two CUs, planned in-kernel over an oversubscribed grid."""
-    return (not latency_bound and max(batch, 1) * num_kv_heads * 2 > num_cus and batch <= PLAN_MAX_BATCH
-            and max_pages < (1 << 23))
+    """Heuristic shape planned in-kernel over an oversubscribed grid: more than one unit per two CUs,
+    or more than one per four CUs where two static splits per unit leave CUs idle."""
+    units = max(batch, 1) * num_kv_heads
+    many = units * 2 > num_cus or (units * 4 > num_cus and units * 2 < num_cus)
+    return not latency_bound and many and batch <= PLAN_MAX_BATCH and max_pages < (1 << 23)
 
 
 def workspace_bytes(batch: int, num_kv_heads: int, gqa: int, head_dim: int, num_splits: int) -> int:

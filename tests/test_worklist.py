@@ -3,8 +3,10 @@
 GPU: a decode run from a work list must return exactly (bit for bit) what the
 same call returns when the kernel plans its items itself, for every way the
 launcher picks items: the in-kernel planner on ragged batches (up to 64 and
-past 64 sequences), the oversubscribed one-item-per-unit plan, the static
-split (full batches, an explicit num_splits), empty sequences, block modes
+past 64 sequences), the oversubscribed grid (one item per unit, or two
+static splits per unit on the first workgroups, for full rows; chunks over
+the whole grid for ragged ones), the static split (full batches, an
+explicit num_splits), empty sequences, block modes
 other than whole-page blocks, and the CSR index.  One list serves several
 runs with different q/K/V; a list planned for another split count is
 detected and ignored; a list planned from other sequence lengths leaves the
@@ -56,6 +58,10 @@ def test_worklist_bytes_is_header_plus_one_record_per_workgroup(batch, hkv, num_
 
 
 # ---------------------------------------------------------------- GPU
+def _extra_cols(kind):
+    return 0 if kind.endswith("_exact") else 1
+
+
 def _dense_case(lens, hkv, group, d, ps, seed, extra_cols=1):
     bt, num_pages = shuffled_table(lens, ps, spare_pages=3, extra_cols=extra_cols, seed=seed)
     k, v = make_cache(num_pages, ps, hkv, d, seed, dtype=torch.float16)
@@ -76,6 +82,12 @@ def _lens(kind, seed):
         return [rng.randint(1, 700) for _ in range(200)], 16
     if kind == "oversub_full":
         return [640] * 200, 16
+    if kind == "oversub_exact":  # every row exactly full (no spare column): one item per unit
+        return [640] * 200, 16
+    if kind == "mid":  # 65-127 units: the oversubscribed grid, chunks over all of it
+        return [rng.randint(1, 4096) for _ in range(48)], 16
+    if kind == "mid_exact":  # the same grid, rows exactly full: two static splits per unit
+        return [2048] * 48, 16
     if kind == "full16":  # every sequence at capacity: the static split
         return [4096] * 16, 16
     if kind == "empty":
@@ -99,6 +111,10 @@ GPU_CASES = [
     ("oversub_full", 2, 6, 96, 16, None),
     ("oversub_full", 2, 4, 32, 16, None),
     ("oversub", 2, 6, 96, 16, None),
+    ("oversub_exact", 2, 6, 128, 16, None),
+    ("mid", 2, 6, 128, 16, None),
+    ("mid_exact", 2, 6, 128, 16, None),
+    ("mid_exact", 2, 6, 96, 16, None),  # head pairing off on this grid
     ("full16", 2, 6, 128, 16, None),
     ("empty", 2, 6, 128, 16, None),
     ("empty", 2, 6, 64, 8, None),  # sub-page blocks
@@ -114,7 +130,7 @@ def test_planned_run_equals_in_kernel_plan(kind, hkv, group, d, ps, num_splits):
     import paged_attention_decode_amd as pad
 
     lens, seed = _lens(kind, 11)[0], 11
-    q, k, v, bt, sl = _dense_case(lens, hkv, group, d, ps, seed)
+    q, k, v, bt, sl = _dense_case(lens, hkv, group, d, ps, seed, _extra_cols(kind))
     w = pad.BatchDecodeWrapper()
     w.plan_block_table(bt, sl, q.shape[1], hkv, d, ps, num_splits=num_splits)
     out = w.run(q, (k, v))
@@ -310,14 +326,16 @@ def _check_plan_structure(wl, lens, ps, hkv, bt_rows, nw, max_pages):
                                            ("empty", 16, False, 128), ("allempty", 16, False, 128),
                                            ("ragged32", 32, True, 128), ("empty", 8, True, 128),
                                            ("oversub_full", 16, False, 96), ("oversub_full", 16, False, 32),
-                                           ("oversub", 16, False, 96), ("ragged32", 32, False, 96)])
+                                           ("oversub", 16, False, 96), ("ragged32", 32, False, 96),
+                                           ("oversub_exact", 16, False, 128), ("mid", 16, False, 128),
+                                           ("mid_exact", 16, False, 128), ("mid_exact", 16, False, 96)])
 def test_work_list_covers_every_page_once(kind, ps, csr, d):
     import paged_attention_decode_amd as pad
     from paged_attention_decode_amd._native import ext
 
     lens, seed = _lens(kind, 31)
     hkv, group = 2, 6
-    q, k, v, bt, sl = _dense_case(lens, hkv, group, d, ps, seed)
+    q, k, v, bt, sl = _dense_case(lens, hkv, group, d, ps, seed, _extra_cols(kind))
     if csr:
         indptr, indices, last = pad.paged_kv_indices(bt, sl, ps)
         plan = lambda: ext().plan_worklist_csr(indptr, indices, last, hkv * group, hkv, d, ps, 0)  # noqa: E731
