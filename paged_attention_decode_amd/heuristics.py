@@ -10,8 +10,9 @@ large batches (profiles/notes.md:875-883 of the reference).
 Inputs are shapes only (no ``seq_lens`` read, so no device sync):
 batch, kv heads, head_dim, page_size, ``max_pages = block_table.shape[1]``
 and the CU count.  Fitted to measured split-count sweeps of configurations
-C2 (batch 1-64), C3 and C4 on MI355X: a power-of-two split count with at
-least 16 blocks of 16 tokens per split; bandwidth-bound shapes get one
+C2 (batch 1-64), C3 and C4 on MI355X: a power-of-two split count (or the
+largest count that fits the workgroup budget, where that is 1.5 times as
+many or more) with at least 16 blocks of 16 tokens per split; bandwidth-bound shapes get one
 4-wave workgroup per CU, latency-bound ones (at most 16 blocks of work per
 CU) 8-wave workgroups on at most half the CUs.  Bandwidth-bound shapes with
 more than one (sequence, kv head) unit per two CUs and batch <= 256 get a grid of
@@ -92,6 +93,9 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
         want = 1
         while want * 2 * units <= max_groups:
             want *= 2
+        fit = max_groups // units
+        if 2 * fit >= 3 * want:  # the largest count that fits, where it is 1.5x the power of two or more
+            want = fit
         if oversubscribed(batch, num_kv_heads, max_pages, latency_bound, num_cus):
             want = max(OVERSUBSCRIBE_SPLITS, _cdiv(OVERSUBSCRIBE_GROUPS_PER_CU * num_cus, units))
         cap = blocks_per_seq // MIN_BLOCKS

@@ -255,6 +255,11 @@ def test_heuristic_properties():
     assert heuristics.plan(96, 12, 2, 128, 16, 256).num_splits == 11  # 192 units: 2112 workgroups
     assert heuristics.plan(65, 12, 2, 128, 16, 256).num_splits == 16  # 130 units
     assert heuristics.plan(64, 12, 2, 128, 16, 256).num_splits == 2  # 128 units: C2 batch 64
+    # The largest split count that fits the workgroup budget replaces the power of two where it is
+    # 1.5 times as large or more: batch 20 (40 units) 6 splits, 17 -> 7, 5 (latency-bound, half the
+    # CUs) -> 12; batch 12 (24 units: 10 against 8) and 7 (9 against 8) keep the power of two.
+    for b, s in ((20, 6), (17, 7), (5, 12), (12, 8), (7, 8), (24, 4), (32, 4)):
+        assert heuristics.plan(b, 12, 2, 128, 16, 256).num_splits == s, b
     p_over = heuristics.plan(512, 12, 2, 128, 16, 256)
     assert p_over.num_splits == 1 and p_over.single_pass
 
