@@ -114,9 +114,9 @@ struct Phase1Args {
   int ps_shift;    // log2(ps) when ps is a power of two, else -1
   int csr;         // 1: page ids from (indptr, indices, last_page_len)
   int balance;     // 1: items planned from the sequence lengths in-kernel;
-                   // 2: the same on an oversubscribed grid (the static
-                   //    splits, pps pages each, on the first workgroups
-                   //    when every sequence is full)
+                   // 2-4: the same on an oversubscribed grid (balance - 1
+                   //    static splits per unit, pps pages each, on the
+                   //    first workgroups when every sequence is full)
   int min_chunk;   // planner: fewest pages per item
   int pair_heads;  // 1: workgroups 8 apart take kv heads 2m and 2m+1 (see grid_pos)
   int wl_key;      // key of the launch's plan, matched against the work list's header
@@ -1276,7 +1276,7 @@ __device__ __forceinline__ WorkItem static_item(const Phase1Args& a, int s, int 
 
 // Planned mode: read every sequence length; with every sequence at full
 // capacity the static split is already even (balance == 1) or, on an
-// oversubscribed grid (balance == 2), the static splits run on the first
+// oversubscribed grid (balance >= 2), the static splits run on the first
 // workgroups (one item per unit, workgroup g = unit, when the static rule
 // gives one split) and the other workgroups exit; otherwise plan the items.
 template <int NK>
@@ -1288,51 +1288,34 @@ __device__ __forceinline__ WorkItem resolve_item(const Phase1Args& a, const SeqR
   for (int k = 0; k < NK; ++k)
     if (lane + 64 * k < a.batch && t.pages[k] != a.max_pages) full = false;
   if (__builtin_amdgcn_ballot_w64(!full) == 0) {
-    const int s0 = a.balance == 2 && a.pps > 0 && a.max_pages > a.pps ? (a.max_pages + a.pps - 1) / a.pps : 1;
-    if (s0 > 1) {
-      // The static splits, s0 per unit (pps pages each), on the first
-      // units * s0 workgroups in order: unit g / s0, split g % s0, whose
-      // partials take the unit's s0 consecutive slots.  The launch keeps
-      // head pairing off here, so g is the linear workgroup index and the
-      // active workgroups spread over the XCDs.
+    if (a.balance >= 2) {
+      // The static splits, s0 per unit of pps pages, on the first units * s0
+      // workgroups in order: unit g / s0, split g mod s0, whose partials
+      // take the unit's s0 consecutive slots (the launch keeps head pairing
+      // off when s0 > 1, so g is the linear index and the active workgroups
+      // spread over the XCDs).  With s0 = 1 (pps = max_pages) each unit is
+      // one item that writes the output rows and never a partial, so its
+      // slot is the workgroup's own (g, which the work list's record check
+      // expects); with pair_heads, units 2r and 2r+1 (kv heads 2m, 2m+1 of
+      // one sequence) then go to workgroups 8 apart, as grid_pos does for
+      // splits.
       WorkItem w;
       const int units = a.batch * a.hkv;
-      const int q = g / s0;
+      const int s0 = a.balance - 1;  // 1, 2 or 3 (setup_launch)
+      const bool paired = s0 == 1 && a.pair_heads && units % 16 == 0;
+      const int gu = paired ? 2 * (((lin >> 4) << 3) | (lin & 7)) + ((lin >> 3) & 1) : g;
+      // g / s0 by a shift or a multiply (exact for g < 2^16; G is far below)
+      const int q = s0 == 2 ? g >> 1 : s0 == 3 ? (int)(((uint32_t)g * 43691u) >> 17) : (paired ? (lin < units ? gu : units) : g);
       const int u = min(q, units - 1);
       w.b = u / a.hkv;
       w.kvh = u - w.b * a.hkv;
-      w.p_begin = (g - q * s0) * a.pps;
+      w.p_begin = s0 > 1 ? (g - q * s0) * a.pps : 0;
       w.p_end = min(w.p_begin + a.pps, a.max_pages);
       w.L = seq_lane_value<NK>(t.len, w.b);
-      w.nsplit = s0;
-      w.slot0 = q * s0;
+      w.nsplit = a.max_pages > 0 ? s0 : 0;
+      w.slot0 = s0 > 1 ? q * s0 : g;
       w.col_max = a.max_pages - 1;
       w.valid = q < units;
-      w.ids_row = a.bt + (int64_t)w.b * a.sbb;
-      w.ids_stride = a.sbp;
-      return w;
-    }
-    if (a.balance == 2) {
-      WorkItem w;
-      const int units = a.batch * a.hkv;
-      // With pair_heads, units 2r and 2r+1 (kv heads 2m, 2m+1 of one
-      // sequence) go to workgroups 8 apart, as grid_pos does for splits.
-      const bool paired = a.pair_heads && units % 16 == 0;
-      const int gu = paired ? 2 * (((lin >> 4) << 3) | (lin & 7)) + ((lin >> 3) & 1) : g;
-      const int u = min(paired ? (lin < units ? gu : units - 1) : g, units - 1);
-      w.b = u / a.hkv;
-      w.kvh = u - w.b * a.hkv;
-      w.p_begin = 0;
-      w.p_end = a.max_pages;
-      w.L = seq_lane_value<NK>(t.len, w.b);
-      w.nsplit = a.max_pages > 0 ? 1 : 0;
-      // The item is its unit's only one, so it writes the output rows and
-      // never a partial: its slot is the workgroup's own (g, which the work
-      // list's record check expects), not the unit index, which differs from
-      // g under pair_heads.
-      w.slot0 = g;
-      w.col_max = a.max_pages - 1;
-      w.valid = (paired ? lin : g) < units;
       w.ids_row = a.bt + (int64_t)w.b * a.sbb;
       w.ids_stride = a.sbp;
       return w;
@@ -2160,10 +2143,18 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   if (a.balance == 2) {
     // An oversubscribed grid runs the static splits when every sequence is
     // at full capacity: pps is theirs (the grid's own split is the planner's
-    // business).  With more than one static split per unit they take the
-    // first workgroups in order, unit-major, so head pairing stays off.
-    a.pps = pps_full;
-    if (ceil_div(d->max_pages, pps_full) > 1) a.pair_heads = 0;
+    // business), and balance = 1 + their count s0 per unit.  More than one
+    // unit per four CUs leaves at most 3 (the budget over the units); with
+    // more than one they take the first workgroups in order, unit-major,
+    // so head pairing stays off.
+    const int s0 = pps_full > 0 && d->max_pages > pps_full ? ceil_div(d->max_pages, pps_full) : 1;
+    if (s0 <= 3) {
+      a.pps = pps_full;
+      a.balance = 1 + s0;
+      if (s0 > 1) a.pair_heads = 0;
+    } else {
+      a.balance = 1;  // not reached; the planner of the grid as it is
+    }
   }
   a.ps_shift = -1;
   for (int sh = 0; sh < 31; ++sh)

@@ -127,21 +127,23 @@ def test_folds_of_many_entries(group, d):
         torch.testing.assert_close(out.float(), base, rtol=2e-3, atol=1e-3)
 
 
-@pytest.mark.parametrize("full,d", [(True, 128), (False, 128), (True, 96), (False, 96), (True, 64)])
-def test_oversubscribed_grid_below_one_unit_per_two_cus(full, d):
-    # 96 units (48 sequences x 2 kv heads) on 256 CUs: the heuristic grid
-    # holds several items per unit.  Rows at full capacity run the two
-    # static splits per unit on its first workgroups (head pairing off at
-    # head_dim 96); ragged rows run equal page chunks over the whole grid.
+@pytest.mark.parametrize("batch,full,d", [(48, True, 128), (48, False, 128), (48, True, 96), (48, False, 96),
+                                          (48, True, 64), (40, True, 128), (40, False, 128), (40, True, 96)])
+def test_oversubscribed_grid_below_one_unit_per_two_cus(batch, full, d):
+    # 96 or 80 units (48 or 40 sequences x 2 kv heads) on 256 CUs: the
+    # heuristic grid holds several items per unit.  Rows at full capacity
+    # run the static splits, two or three per unit, on its first workgroups
+    # (head pairing off at head_dim 96); ragged rows run equal page chunks
+    # over the whole grid.
     from paged_attention_decode_amd.heuristics import plan
 
-    rng = random.Random(77 + d)
-    lens = [2048] * 48 if full else [rng.randint(1, 4096) for _ in range(48)]
-    bt, total = shuffled_table(lens, 16, spare_pages=2, extra_cols=0, seed=78 + d)
+    rng = random.Random(77 + d + batch)
+    lens = [2048] * batch if full else [rng.randint(1, 4096) for _ in range(batch)]
+    bt, total = shuffled_table(lens, 16, spare_pages=2, extra_cols=0, seed=78 + d + batch)
     assert (bt.shape[1] == 128) == full
-    k, v = make_cache(total, 16, 2, d, seed=79 + d)
-    q = torch.randn(48, 12, d, generator=torch.Generator().manual_seed(80 + d))
-    assert plan(48, 12, 2, d, 16, bt.shape[1]).num_splits > 2
+    k, v = make_cache(total, 16, 2, d, seed=79 + d + batch)
+    q = torch.randn(batch, 12, d, generator=torch.Generator().manual_seed(80 + d + batch))
+    assert plan(batch, 12, 2, d, 16, bt.shape[1]).num_splits > 3
     out = _check(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), 0, None)
     for _ in range(2):  # counters back to zero, same bits
         assert torch.equal(_run(q, k, v, bt, torch.tensor(lens, dtype=torch.int32), 0), out)

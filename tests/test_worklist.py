@@ -88,6 +88,8 @@ def _lens(kind, seed):
         return [rng.randint(1, 4096) for _ in range(48)], 16
     if kind == "mid_exact":  # the same grid, rows exactly full: two static splits per unit
         return [2048] * 48, 16
+    if kind == "mid3_exact":  # 80 units, rows exactly full: three static splits per unit
+        return [2048] * 40, 16
     if kind == "full16":  # every sequence at capacity: the static split
         return [4096] * 16, 16
     if kind == "empty":
@@ -115,6 +117,7 @@ GPU_CASES = [
     ("mid", 2, 6, 128, 16, None),
     ("mid_exact", 2, 6, 128, 16, None),
     ("mid_exact", 2, 6, 96, 16, None),  # head pairing off on this grid
+    ("mid3_exact", 2, 6, 128, 16, None),
     ("full16", 2, 6, 128, 16, None),
     ("empty", 2, 6, 128, 16, None),
     ("empty", 2, 6, 64, 8, None),  # sub-page blocks
@@ -328,7 +331,8 @@ def _check_plan_structure(wl, lens, ps, hkv, bt_rows, nw, max_pages):
                                            ("oversub_full", 16, False, 96), ("oversub_full", 16, False, 32),
                                            ("oversub", 16, False, 96), ("ragged32", 32, False, 96),
                                            ("oversub_exact", 16, False, 128), ("mid", 16, False, 128),
-                                           ("mid_exact", 16, False, 128), ("mid_exact", 16, False, 96)])
+                                           ("mid_exact", 16, False, 128), ("mid_exact", 16, False, 96),
+                                           ("mid3_exact", 16, False, 128)])
 def test_work_list_covers_every_page_once(kind, ps, csr, d):
     import paged_attention_decode_amd as pad
     from paged_attention_decode_amd._native import ext
