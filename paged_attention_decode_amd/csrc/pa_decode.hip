@@ -1796,9 +1796,16 @@ constexpr int kOversubscribeGroupsPerCu = 8;
 // 34-46 us planned).  The launch therefore sizes the grid for several items
 // per unit and the kernel decides from the lengths: all at full capacity,
 // the static splits on the first workgroups; otherwise equal page chunks.
-static bool oversubscribed_shape(const pad_decode_dims* d, int num_splits, int num_cus, bool latency_bound) {
+// fp8 caches (kv_bytes 1) keep the regime from one unit per CU up: their
+// items carry half the bytes, and the grids below that (and the 8-per-CU
+// floor of oversubscribe_splits) measured slower for them than the static
+// splits (12/2 heads, lengths up to 4096, batch 40 / 96: 25.7 / 41.1 us
+// against 18.8 / 31.4 us).
+static bool oversubscribed_shape(const pad_decode_dims* d, int num_splits, int num_cus, bool latency_bound,
+                                 int kv_bytes = 2) {
   const int64_t units = (int64_t)(d->batch > 0 ? d->batch : 1) * d->num_kv_heads;
-  const bool many = units * 2 > num_cus || (units * 4 > num_cus && units * 2 < num_cus);
+  const bool many = kv_bytes == 1 ? units >= num_cus
+                                  : units * 2 > num_cus || (units * 4 > num_cus && units * 2 < num_cus);
   return num_splits == 0 && !latency_bound && many && d->batch <= kPlanMaxBatch && d->max_pages < (1 << 23);
 }
 
@@ -1883,7 +1890,14 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
     const int64_t s_fit = max_groups / units;
     if (2 * s_fit >= 3 * s_want) s_want = s_fit;
     int64_t s_static = s_want;
-    if (oversubscribed_shape(d, num_splits, num_cus, latency_bound)) s_want = oversubscribe_splits(units, num_cus);
+    if (oversubscribed_shape(d, num_splits, num_cus, latency_bound, kv_bytes)) {
+      s_want = kv_bytes == 1 ? kOversubscribeSplits : oversubscribe_splits(units, num_cus);
+      // Rows of at most 128 bytes run 8-wave workgroups (below): half as
+      // many items, so that each wave streams as many blocks as in a 4-wave
+      // workgroup (fp16 head_dim 64, 32/8 heads, lengths up to 4096, batch
+      // 20: 30.1 us with the full item count, 25.9 us with half).
+      if (d->head_dim * kv_bytes <= 128 && units <= num_cus && kv_bytes == 2) s_want /= 2;
+    }
     int64_t s_cap = blocks_per_seq / kMinBlocks;
     // Latency-bound short sequences: a wave's serial chain of blocks costs
     // more than a merge of up to 16 splits (one round trip), so splits may
@@ -1918,8 +1932,10 @@ static int plan_impl(const pad_decode_dims* d, int num_splits, int num_cus, int 
   // bytes or less, and 8 waves keep as many bytes in flight per CU (32/8 d64
   // batch 32: 25.8 against 29.9 us; 16/4 d32: 17.8 against 21.9 us).  With
   // more units than CUs, 4-wave workgroups let several units share a CU
-  // (16/16 d64 batch 32: 46.9 against 47.9 us).  The split count does not
-  // depend on kv_bytes, so the scratch sizes do not either.
+  // (16/16 d64 batch 32: 46.9 against 47.9 us).  The split count depends on
+  // kv_bytes only through the oversubscribed regime, which gives fp8 caches
+  // fewer items than fp16 ones, never more, so the fp16 plan's scratch
+  // sizes always cover the fp8 plan's.
   const bool narrow_rows = d->head_dim * kv_bytes <= 128 && units <= num_cus;
   const int nw_max = (latency_bound || narrow_rows) ? kMaxWaves : kMaxWaves / 2;
   if (nw > nw_max) nw = nw_max;
@@ -2136,7 +2152,7 @@ static int setup_launch(const void* q, const void* k, const void* v, const int32
   // keeps its meaning (that many page-aligned splits per sequence).
   a.balance = 0;
   if (num_splits == 0 && !plan.single_pass && d->batch <= kPlanMaxBatch && d->max_pages < (1 << 23))
-    a.balance = oversubscribed_shape(d, num_splits, cus, latency_bound_shape(d, cus, csr)) ? 2 : 1;
+    a.balance = oversubscribed_shape(d, num_splits, cus, latency_bound_shape(d, cus, csr), kv_bytes) ? 2 : 1;
   a.min_chunk = ceil_div(kMinBlocks * kBlockTokens, d->page_size);
   a.pair_heads = ((d->head_dim * 2) % 128 != 0 && d->num_kv_heads % 2 == 0 &&
                   ((int64_t)S * d->num_kv_heads * d->batch) % 16 == 0) ? 1 : 0;

@@ -96,8 +96,13 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
         fit = max_groups // units
         if 2 * fit >= 3 * want:  # the largest count that fits, where it is 1.5x the power of two or more
             want = fit
-        if oversubscribed(batch, num_kv_heads, max_pages, latency_bound, num_cus):
-            want = max(OVERSUBSCRIBE_SPLITS, _cdiv(OVERSUBSCRIBE_GROUPS_PER_CU * num_cus, units))
+        if oversubscribed(batch, num_kv_heads, max_pages, latency_bound, num_cus, kv_bytes):
+            if kv_bytes == 1:  # fp8 caches: the 4-item grid from one unit per CU up
+                want = OVERSUBSCRIBE_SPLITS
+            else:
+                want = max(OVERSUBSCRIBE_SPLITS, _cdiv(OVERSUBSCRIBE_GROUPS_PER_CU * num_cus, units))
+                if head_dim * kv_bytes <= 128 and units <= num_cus:  # 8-wave workgroups: half the items
+                    want //= 2
         cap = blocks_per_seq // MIN_BLOCKS
         if latency_bound:  # short sequences: down to 4 blocks per split, at most 16 splits
             cap = max(cap, min(blocks_per_seq // MIN_BLOCKS_SHORT, 16))
@@ -123,11 +128,16 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     return Plan(s, pps, nw, single, ws, counters)
 
 
-def oversubscribed(batch: int, num_kv_heads: int, max_pages: int, latency_bound: bool, num_cus: int) -> bool:
+def oversubscribed(batch: int, num_kv_heads: int, max_pages: int, latency_bound: bool, num_cus: int,
+                   kv_bytes: int = 2) -> bool:
     """Heuristic shape planned in-kernel over an oversubscribed grid: more than one unit per two CUs,
-    or more than one per four CUs where two static splits per unit leave CUs idle."""
+    or more than one per four CUs where two static splits per unit leave CUs idle (fp8 caches: one
+    unit per CU or more)."""
     units = max(batch, 1) * num_kv_heads
-    many = units * 2 > num_cus or (units * 4 > num_cus and units * 2 < num_cus)
+    if kv_bytes == 1:
+        many = units >= num_cus
+    else:
+        many = units * 2 > num_cus or (units * 4 > num_cus and units * 2 < num_cus)
     return not latency_bound and many and batch <= PLAN_MAX_BATCH and max_pages < (1 << 23)
 
 

@@ -460,8 +460,10 @@ def test_launch_csr_through_c_abi(splits):
 def test_fp8_plan_keeps_the_scratch_of_the_fp16_plan():
     # pad_decode_launch_kv8 plans with one byte per K/V element: the same
     # splits, workspace and counters as pad_decode_plan (which sizes its
-    # scratch), and 8-wave workgroups only where the fp16 plan has 4 waves
-    # for 256-byte rows.
+    # scratch), except where the fp16 plan is an oversubscribed grid: fp8
+    # takes the 4-item grid from one unit per CU up only, so never more
+    # scratch; 8-wave workgroups only where the fp16 plan has 4 waves for
+    # 256-byte rows.
     import random
 
     rng = random.Random(5)
@@ -472,8 +474,15 @@ def test_fp8_plan_keeps_the_scratch_of_the_fp16_plan():
         max_pages = rng.randint(1, 4096) // ps + 1
         a = heuristics.plan(batch, hkv * gqa, hkv, d, ps, max_pages)
         b = heuristics.plan(batch, hkv * gqa, hkv, d, ps, max_pages, kv_bytes=1)
-        assert (a.num_splits, a.pages_per_split, a.single_pass, a.workspace_bytes, a.counters) == (
-            b.num_splits, b.pages_per_split, b.single_pass, b.workspace_bytes, b.counters)
+        units = batch * hkv
+        lat = units * -(-max_pages * ps // 16) <= 16 * 256
+        fewer = heuristics.oversubscribed(batch, hkv, max_pages, lat, 256)  # the fp16 grid
+        if fewer:
+            assert b.num_splits <= a.num_splits and b.workspace_bytes <= a.workspace_bytes
+            assert b.counters <= a.counters
+        else:
+            assert (a.num_splits, a.pages_per_split, a.single_pass, a.workspace_bytes, a.counters) == (
+                b.num_splits, b.pages_per_split, b.single_pass, b.workspace_bytes, b.counters)
         assert b.waves_per_group >= a.waves_per_group
         if d != 128:
             assert b.waves_per_group == a.waves_per_group
