@@ -77,7 +77,8 @@ def plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_si
     """Same result as ``pad_decode_plan`` (``pad_decode_plan_csr`` with ``csr``) for valid arguments.
 
     ``kv_bytes=1`` gives the plan of an fp8-cache launch (pad_decode_launch_kv8): the same splits and
-    scratch, 8-wave workgroups for its 128-byte rows at head_dim 128."""
+    scratch except where the fp16 plan is an oversubscribed grid (fp8 takes the 4-item grid from one
+    unit per CU up only: never more scratch), 8-wave workgroups for its 128-byte rows at head_dim 128."""
     if num_cus <= 0:
         num_cus = 256
     gqa = num_q_heads // num_kv_heads
